@@ -1,0 +1,47 @@
+// Internal interface between the decode entry point and its kernels.
+#pragma once
+
+#include "dc_common.h"
+
+namespace dc {
+
+constexpr int kMaxQ = 16;     // GQA query heads per KV head
+constexpr int kMaxCap = 256;  // page capacity the decode kernels accept
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct DecodeArgs {
+  dc_pool kpool;
+  dc_pool vpool;
+  const int32_t* k_table;
+  const int32_t* v_table;
+  int32_t table_stride;
+  const dc_work_item* items;
+  int32_t n_items;
+  const void* queries;
+  int32_t queries_dtype;
+  float q_scale;
+  int32_t n_kv_heads;
+  int32_t n_q;
+  float* out;
+  float* part_o;    // [max_partials][n_q][head_dim]
+  float* part_ml;   // [max_partials][n_q][2]  (m, l) in the log2 domain
+  int64_t max_partials;
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+int launch_decode(const DecodeArgs& a, hipStream_t stream);
+int launch_decode_generic(const DecodeArgs& a, hipStream_t stream);
+int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream);
+
+}  // namespace dc

@@ -1,0 +1,287 @@
+// Fused paged decode: score -> single-pass online softmax -> mix, straight
+// from compressed pages, plus the split-K log-sum-exp merge.
+//
+// This file holds the generic path, which reads every page format the pool
+// can hold (M0 affine / symmetric 2/3/4/8-bit, any group size, both layouts;
+// M3 fp16 / fp32 / int8) and up to kMaxQ GQA query heads per KV head.  The
+// MFMA fast path for the common formats lives in dc_decode_mfma.hip and is
+// chosen by dc_decode_paged when every page of the call fits it.
+//
+// Semantics: reference dotcache/attention_runtime.py:260-315 (concatenate
+// page logits, one softmax over the whole context, mix every value page)
+// computed as the online softmax of reference
+// dotcache/backends/torch_mps.py:4331-4435 (running max m, running sum l,
+// rescale by exp(m_old - m_new), divide at the end).  Exponentials are
+// taken base 2 on logits pre-multiplied by log2(e).
+#include "dc_common.h"
+#include "dc_decode.h"
+
+namespace dc {
+
+constexpr int kThreads = 256;
+constexpr int kMaxHD = 256;
+constexpr int kTokChunk = 64;
+constexpr int kParts = kThreads / kTokChunk;  // channel partitions in the score phase
+constexpr int kMaxGroups = 64;
+
+__device__ __forceinline__ float score_partial_m0(const uint8_t* blob, const dc_page_desc& d, const BlobLayout& L,
+                                                  const dc_page_geometry& geo, int32_t t, int32_t part,
+                                                  const float* __restrict__ qs, const float* __restrict__ qsum,
+                                                  int32_t phd, int32_t nq, float* acc) {
+  const uint32_t* payload = reinterpret_cast<const uint32_t*>(blob);
+  const __half* sc = reinterpret_cast<const __half*>(blob + L.scales_off);
+  const __half* bs = reinterpret_cast<const __half*>(blob + L.bias_off);
+  const int32_t G = L.groups, gs = geo.group_size;
+  const float zp = float((1 << (d.bits - 1)) - 1);
+  for (int32_t g = part; g < G; g += kParts) {
+    float dot[kMaxQ];
+#pragma unroll
+    for (int j = 0; j < kMaxQ; ++j) dot[j] = 0.f;
+    for (int32_t k = 0; k < gs; ++k) {
+      float code = float(m0_code(payload, t, g, k, d.bits, L.words, G, geo.page_capacity, geo.layout));
+      if (d.format == DC_FMT_M0_SYMMETRIC) code -= zp;
+      const int32_t c = g * gs + k;
+#pragma unroll
+      for (int j = 0; j < kMaxQ; ++j)
+        if (j < nq) dot[j] += code * qs[j * phd + c];
+    }
+    const float s = __half2float(sc[t * G + g]);
+    const float b = d.format == DC_FMT_M0_AFFINE ? __half2float(bs[t * G + g]) : 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxQ; ++j)
+      if (j < nq) acc[j] += s * dot[j] + b * qsum[j * G + g];
+  }
+  return 0.f;
+}
+
+__global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) {
+  const dc_work_item it = a.items[blockIdx.x];
+  const dc_page_geometry geo = a.kpool.geometry, vgeo = a.vpool.geometry;
+  const int32_t hd = geo.head_dim, gs = geo.group_size;
+  const int32_t G = (hd + gs - 1) / gs, phd = G * gs;
+  const int32_t nq = a.n_q;
+  const int32_t tid = threadIdx.x;
+
+  __shared__ float qs[kMaxQ * kMaxHD];        // scaled queries, zero padded to phd
+  __shared__ float qsum[kMaxQ * kMaxGroups];  // per-group query sums
+  __shared__ float red[kParts][kMaxQ][kTokChunk];
+  __shared__ float prob[kMaxQ][kMaxCap];
+  __shared__ float m_run[kMaxQ], l_run[kMaxQ], alpha[kMaxQ];
+
+  // queries: [seq, kv_head, q, hd]
+  const int64_t qbase = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * nq * hd;
+  for (int32_t i = tid; i < nq * phd; i += kThreads) {
+    const int32_t j = i / phd, c = i - j * phd;
+    qs[j * phd + c] = c < hd ? load_value(a.queries, a.queries_dtype, qbase + int64_t(j) * hd + c) * a.q_scale : 0.f;
+  }
+  __syncthreads();
+  for (int32_t i = tid; i < nq * G; i += kThreads) {
+    const int32_t j = i / G, g = i - j * G;
+    float s = 0.f;
+    for (int32_t k = 0; k < gs; ++k) s += qs[j * phd + g * gs + k];
+    qsum[j * G + g] = s;
+  }
+  if (tid < kMaxQ) {
+    m_run[tid] = -INFINITY;
+    l_run[tid] = 0.f;
+    alpha[tid] = 1.f;
+  }
+  float acc[kMaxQ];
+#pragma unroll
+  for (int j = 0; j < kMaxQ; ++j) acc[j] = 0.f;
+  __syncthreads();
+
+  const int64_t trow = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * a.table_stride;
+  for (int32_t p = it.page_begin; p < it.page_end; ++p) {
+    const int32_t kid = a.k_table[trow + p], vid = a.v_table[trow + p];
+    if (kid < 0 || kid >= a.kpool.n_descs || vid < 0 || vid >= a.vpool.n_descs) continue;
+    const dc_page_desc kd = a.kpool.descs[kid], vd = a.vpool.descs[vid];
+    const BlobLayout KL = blob_layout(kd.format, kd.bits, geo), VL = blob_layout(vd.format, vd.bits, vgeo);
+    if ((int64_t(kd.block) << 8) + KL.total > a.kpool.arena_bytes) continue;
+    if ((int64_t(vd.block) << 8) + VL.total > a.vpool.arena_bytes) continue;
+    int32_t T = kd.tokens < vd.tokens ? kd.tokens : vd.tokens;
+    if (T > geo.page_capacity) T = geo.page_capacity;
+    if (T <= 0) continue;
+    const uint8_t* kb = blob_ptr(a.kpool.arena, kd);
+    const uint8_t* vb = blob_ptr(a.vpool.arena, vd);
+
+    // ---- score: thread (token, part); parts split the channels ----
+    for (int32_t t0 = 0; t0 < T; t0 += kTokChunk) {
+      const int32_t t = t0 + (tid % kTokChunk), part = tid / kTokChunk;
+      float s[kMaxQ];
+#pragma unroll
+      for (int j = 0; j < kMaxQ; ++j) s[j] = 0.f;
+      if (t < T) {
+        if (is_m0(kd.format)) {
+          score_partial_m0(kb, kd, KL, geo, t, part, qs, qsum, phd, nq, s);
+        } else {
+          for (int32_t c = part; c < hd; c += kParts) {
+            const float v = page_value(kb, kd, KL, geo, t, c);
+#pragma unroll
+            for (int j = 0; j < kMaxQ; ++j)
+              if (j < nq) s[j] += v * qs[j * phd + c];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMaxQ; ++j) red[part][j][tid % kTokChunk] = s[j];
+      __syncthreads();
+      for (int32_t i = tid; i < nq * kTokChunk; i += kThreads) {
+        const int32_t j = i / kTokChunk, tt = i - j * kTokChunk;
+        if (t0 + tt < T) prob[j][t0 + tt] = (red[0][j][tt] + red[1][j][tt] + red[2][j][tt] + red[3][j][tt]) * kLog2e;
+      }
+      __syncthreads();
+    }
+
+    // ---- online softmax: one wave per query head ----
+    const int32_t wave = tid / 64, lane = tid % 64;
+    for (int32_t j = wave; j < nq; j += kThreads / 64) {
+      float mx = -INFINITY;
+      for (int32_t t = lane; t < T; t += 64) mx = fmaxf(mx, prob[j][t]);
+      mx = wave_max(mx);
+      const float m_old = m_run[j];
+      const float m_new = fmaxf(m_old, mx);
+      float sum = 0.f;
+      for (int32_t t = lane; t < T; t += 64) {
+        const float e = exp2f(prob[j][t] - m_new);
+        prob[j][t] = e;
+        sum += e;
+      }
+      sum = wave_sum(sum);
+      if (lane == 0) {
+        const float al = exp2f(m_old - m_new);
+        alpha[j] = al;
+        l_run[j] = l_run[j] * al + sum;
+        m_run[j] = m_new;
+      }
+    }
+    __syncthreads();
+
+    // ---- mix: one thread per channel (hd <= kThreads is checked on the host) ----
+    if (tid < hd) {
+      const int32_t c = tid;
+#pragma unroll
+      for (int j = 0; j < kMaxQ; ++j) acc[j] *= alpha[j];
+      for (int32_t t = 0; t < T; ++t) {
+        const float v = page_value(vb, vd, VL, vgeo, t, c);
+#pragma unroll
+        for (int j = 0; j < kMaxQ; ++j)
+          if (j < nq) acc[j] += prob[j][t] * v;
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- write the normalised output or a split-K partial ----
+  if (it.partial >= a.max_partials) return;
+  if (tid < hd) {
+    if (it.partial < 0) {
+      float* o = a.out + qbase + tid;
+#pragma unroll
+      for (int j = 0; j < kMaxQ; ++j)
+        if (j < nq) o[int64_t(j) * hd] = acc[j] / fmaxf(l_run[j], 1e-30f);
+    } else {
+      float* o = a.part_o + int64_t(it.partial) * nq * hd + tid;
+#pragma unroll
+      for (int j = 0; j < kMaxQ; ++j)
+        if (j < nq) o[int64_t(j) * hd] = acc[j];
+    }
+  }
+  if (it.partial >= 0 && tid < nq) {
+    a.part_ml[(int64_t(it.partial) * nq + tid) * 2 + 0] = m_run[tid];
+    a.part_ml[(int64_t(it.partial) * nq + tid) * 2 + 1] = l_run[tid];
+  }
+}
+
+// One block per merge item, one thread per channel: combine partials s with
+// weights exp2(m_s - M) (log2 domain), then divide by the merged sum.
+__global__ void __launch_bounds__(256) merge_kernel(const dc_merge_item* __restrict__ merges, const float* part_o,
+                                                    const float* part_ml, float* out, int32_t n_kv_heads,
+                                                    int32_t nq, int32_t hd, int64_t max_partials) {
+  const dc_merge_item mi = merges[blockIdx.x];
+  const int32_t j = blockIdx.y;
+  if (mi.partial_begin < 0 || mi.count <= 0 || mi.partial_begin + mi.count > max_partials) return;
+  for (int32_t c = threadIdx.x; c < hd; c += blockDim.x) {
+    float M = -INFINITY;
+    for (int32_t s = 0; s < mi.count; ++s) M = fmaxf(M, part_ml[(int64_t(mi.partial_begin + s) * nq + j) * 2]);
+    float L = 0.f, O = 0.f;
+    for (int32_t s = 0; s < mi.count; ++s) {
+      const int64_t ps = mi.partial_begin + s;
+      const float m = part_ml[(ps * nq + j) * 2], l = part_ml[(ps * nq + j) * 2 + 1];
+      const float w = m == -INFINITY ? 0.f : exp2f(m - M);
+      L += l * w;
+      O += part_o[(ps * nq + j) * hd + c] * w;
+    }
+    out[((int64_t(mi.seq) * n_kv_heads + mi.kv_head) * nq + j) * hd + c] = O / fmaxf(L, 1e-30f);
+  }
+}
+
+int launch_decode_generic(const DecodeArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(decode_generic_kernel, dim3(uint32_t(a.n_items)), dim3(kThreads), 0, stream, a);
+  return check_hip(hipGetLastError(), "decode_generic_kernel launch");
+}
+
+int launch_decode(const DecodeArgs& a, hipStream_t stream) { return launch_decode_generic(a, stream); }
+
+int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream) {
+  if (n_merges <= 0) return DC_OK;
+  hipLaunchKernelGGL(merge_kernel, dim3(uint32_t(n_merges), uint32_t(a.n_q)), dim3(256), 0, stream, merges,
+                     a.part_o, a.part_ml, a.out, a.n_kv_heads, a.n_q, a.kpool.geometry.head_dim, a.max_partials);
+  return check_hip(hipGetLastError(), "merge_kernel launch");
+}
+
+}  // namespace dc
+
+extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table, int32_t table_stride,
+                               const dc_work_item* items, int32_t n_items, const dc_merge_item* merges,
+                               int32_t n_merges, const void* queries, int32_t queries_dtype, float query_scale,
+                               int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, float* out, void* workspace,
+                               int64_t workspace_bytes, dc_stream_t stream) {
+  if (int rc = dc::validate_geometry(k_pool.geometry)) return rc;
+  if (int rc = dc::validate_geometry(v_pool.geometry)) return rc;
+  const dc_page_geometry& g = k_pool.geometry;
+  if (v_pool.geometry.head_dim != g.head_dim || v_pool.geometry.page_capacity != g.page_capacity)
+    return dc::fail(DC_EINVAL, "key and value pools must share head_dim and page_capacity");
+  if (n_items < 0 || n_merges < 0 || n_seqs <= 0 || n_kv_heads <= 0)
+    return dc::fail(DC_EINVAL, "dc_decode_paged: bad counts");
+  if (n_q <= 0 || n_q > dc::kMaxQ) return dc::fail(DC_EINVAL, "n_q must be in [1, %d]", dc::kMaxQ);
+  if (g.head_dim > dc::kMaxHD) return dc::fail(DC_EINVAL, "head_dim %d exceeds %d", g.head_dim, dc::kMaxHD);
+  if (dc::num_groups(g) > dc::kMaxGroups || dc::num_groups(v_pool.geometry) > dc::kMaxGroups) return dc::fail(DC_EINVAL, "more than %d groups per head", dc::kMaxGroups);
+  if (g.page_capacity > dc::kMaxCap)
+    return dc::fail(DC_EINVAL, "page_capacity %d exceeds %d for decode", g.page_capacity, dc::kMaxCap);
+  if (queries_dtype != DC_F32 && queries_dtype != DC_F16 && queries_dtype != DC_BF16)
+    return dc::fail(DC_EINVAL, "queries_dtype must be DC_F32, DC_F16 or DC_BF16");
+  if (n_items == 0) return DC_OK;
+  if (!k_table || !v_table || !items || !queries || !out || !k_pool.arena || !k_pool.descs || !v_pool.arena ||
+      !v_pool.descs)
+    return dc::fail(DC_EINVAL, "dc_decode_paged: null pointer");
+  if (n_merges > 0 && !merges) return dc::fail(DC_EINVAL, "dc_decode_paged: null merges");
+
+  dc::DecodeArgs a{};
+  a.kpool = k_pool;
+  a.vpool = v_pool;
+  a.k_table = k_table;
+  a.v_table = v_table;
+  a.table_stride = table_stride;
+  a.items = items;
+  a.n_items = n_items;
+  a.queries = queries;
+  a.queries_dtype = queries_dtype;
+  a.q_scale = query_scale;
+  a.n_kv_heads = n_kv_heads;
+  a.n_q = n_q;
+  a.out = out;
+  // the workspace holds as many partial slots as fit; kernels skip any
+  // item or merge naming a slot past that count
+  const int64_t per_partial = int64_t(n_q) * (g.head_dim + 2) * 4;
+  const int64_t n_partials = per_partial > 0 ? workspace_bytes / per_partial : 0;
+  a.part_o = reinterpret_cast<float*>(workspace);
+  a.part_ml = a.part_o + n_partials * n_q * g.head_dim;
+  a.max_partials = n_partials;
+  if (n_merges > 0 && (!workspace || n_partials <= 0))
+    return dc::fail(DC_ESPACE, "dc_decode_paged: split-K items need a workspace");
+
+  int rc = dc::launch_decode(a, hipStream_t(stream));
+  if (rc) return rc;
+  return dc::launch_merge(a, merges, n_merges, hipStream_t(stream));
+}

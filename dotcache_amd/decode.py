@@ -1,0 +1,163 @@
+"""Host driver of the fused paged decode kernel (``dc_decode_paged``).
+
+A decode call covers a batch of sequences x KV heads of one layer.  Page
+tables are int32 ``[n_seqs, n_kv_heads, table_stride]`` arrays of page ids in
+one :class:`~dotcache_amd.page_pool.DevicePagePool`; sequences may have
+different page counts (ragged batch) and their pages may sit anywhere in the
+arena.  The host planner (``dc_plan_decode``) splits long page lists into
+work items of ``pages_per_split`` pages (split-K); the kernel writes
+``(m, l, o)`` partials for split items and the merge pass combines them by
+log-sum-exp.  Plans are cached per (page counts, heads, split) so a steady
+decode loop uploads nothing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .page_pool import DevicePagePool, current_stream_ptr, dtype_code
+
+# Split long page lists so a launch has enough work items to fill the
+# 256 CUs, but keep each item long enough to amortise its setup.
+DEFAULT_TARGET_ITEMS = 2048
+MIN_PAGES_PER_SPLIT = 8
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+@dataclass
+class DecodePlan:
+    items: object          # device uint8 tensor holding dc_work_item[n_items]
+    merges: object | None  # device uint8 tensor holding dc_merge_item[n_merges]
+    n_items: int
+    n_merges: int
+    n_partials: int
+    pages_per_split: int
+    host_items: np.ndarray
+
+
+_plan_cache: dict = {}
+
+
+def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items: int = DEFAULT_TARGET_ITEMS) -> int:
+    """Pages per work item so that the launch has about ``target_items`` items."""
+    total = int(np.sum(seq_pages)) * n_kv_heads
+    per = max(MIN_PAGES_PER_SPLIT, -(-total // max(target_items, 1)))
+    return int(min(per, max(int(np.max(seq_pages)), 1)))
+
+
+def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *, device="cuda") -> DecodePlan:
+    torch = _torch()
+    sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
+    if sp.ndim != 1 or sp.size == 0:
+        raise ValueError("seq_pages must be a non-empty 1-D array")
+    if np.any(sp <= 0):
+        raise ValueError("decode requires at least one page per sequence")
+    pps = choose_pages_per_split(sp, n_kv_heads) if pages_per_split is None else int(pages_per_split)
+    key = (sp.tobytes(), int(n_kv_heads), pps, str(device))
+    hit = _plan_cache.get(key)
+    if hit is not None:
+        return hit
+    L = _lib.lib()
+    ni, nm, npart = C.c_int32(), C.c_int32(), C.c_int32()
+    st = L.dc_plan_decode(sp.ctypes.data, sp.size, n_kv_heads, pps, None, 0, C.byref(ni), None, 0, C.byref(nm), C.byref(npart))
+    if st not in (_lib.DC_OK, _lib.DC_ESPACE):
+        _lib.check(st, "dc_plan_decode")
+    items = (_lib.WorkItem * max(ni.value, 1))()
+    merges = (_lib.MergeItem * max(nm.value, 1))()
+    st = L.dc_plan_decode(sp.ctypes.data, sp.size, n_kv_heads, pps, C.addressof(items), ni.value, C.byref(ni),
+                          C.addressof(merges), nm.value, C.byref(nm), C.byref(npart))
+    _lib.check(st, "dc_plan_decode")
+    host_items = np.frombuffer(bytes(items), dtype=np.int32).reshape(-1, 8)[: ni.value].copy()
+    dev_items = torch.frombuffer(bytearray(bytes(items)), dtype=torch.uint8).to(device)
+    dev_merges = torch.frombuffer(bytearray(bytes(merges)), dtype=torch.uint8).to(device) if nm.value else None
+    plan = DecodePlan(dev_items, dev_merges, ni.value, nm.value, npart.value, pps, host_items)
+    if len(_plan_cache) > 256:
+        _plan_cache.clear()
+    _plan_cache[key] = plan
+    return plan
+
+
+def workspace_bytes(plan: DecodePlan, n_q: int, head_dim: int) -> int:
+    return int(_lib.lib().dc_decode_workspace_bytes(plan.n_partials, n_q, head_dim))
+
+
+def decode_paged(
+    pool: DevicePagePool,
+    k_table,
+    v_table,
+    seq_pages,
+    queries,
+    *,
+    query_scale: float = 1.0,
+    pages_per_split: int | None = None,
+    plan: DecodePlan | None = None,
+    out=None,
+    workspace=None,
+    validate: bool = True,
+    v_pool: DevicePagePool | None = None,
+):
+    """Fused decode for ``queries [n_seqs, n_kv_heads, n_q, head_dim]``.
+
+    ``pool`` holds the key pages and, unless ``v_pool`` is given, the value
+    pages too (the two pools may differ in group size only).
+
+    Returns ``out`` fp32 ``[n_seqs, n_kv_heads, n_q, head_dim]``.
+    ``seq_pages[b]`` is the number of pages of sequence b (the first
+    entries of its page-table rows).
+    """
+    torch = _torch()
+    vpool = pool if v_pool is None else v_pool
+    if (vpool.geometry.head_dim, vpool.geometry.page_capacity) != (pool.geometry.head_dim, pool.geometry.page_capacity):
+        raise ValueError("key and value pools must share head_dim and page_capacity")
+    if queries.dim() != 4:
+        raise ValueError("queries must have shape [n_seqs, n_kv_heads, n_q, head_dim]")
+    B, H, Q, hd = (int(x) for x in queries.shape)
+    if hd != pool.geometry.head_dim:
+        raise ValueError("queries head_dim does not match the pool geometry")
+    if tuple(k_table.shape[:2]) != (B, H) or tuple(v_table.shape) != tuple(k_table.shape):
+        raise ValueError("page tables must have shape [n_seqs, n_kv_heads, table_stride]")
+    if k_table.dtype != torch.int32 or v_table.dtype != torch.int32:
+        raise ValueError("page tables must be int32")
+    sp = np.asarray(seq_pages, dtype=np.int32)
+    if sp.shape != (B,):
+        raise ValueError("seq_pages must have one entry per sequence")
+    stride = int(k_table.shape[2])
+    if np.any(sp > stride):
+        raise ValueError("seq_pages exceeds the page-table width")
+    if validate:
+        kt = k_table.cpu().numpy()
+        vt = v_table.cpu().numpy()
+        for b in range(B):
+            ids_k = kt[b, :, : sp[b]]
+            ids_v = vt[b, :, : sp[b]]
+            pool.validate_ids(ids_k)
+            vpool.validate_ids(ids_v)
+            if not np.array_equal(pool.tokens_of(ids_k), vpool.tokens_of(ids_v)):
+                raise ValueError("key and value pages must hold the same token counts")
+    if plan is None:
+        plan = make_plan(sp, H, pages_per_split, device=queries.device)
+    if not queries.is_contiguous():
+        queries = queries.contiguous()
+    if out is None:
+        out = torch.empty((B, H, Q, hd), dtype=torch.float32, device=queries.device)
+    need = workspace_bytes(plan, Q, hd)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=queries.device)
+    st = _lib.lib().dc_decode_paged(
+        pool.c_pool(), vpool.c_pool(), C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
+        C.c_void_p(plan.items.data_ptr()), plan.n_items,
+        C.c_void_p(plan.merges.data_ptr() if plan.merges is not None else 0), plan.n_merges,
+        C.c_void_p(queries.data_ptr()), dtype_code(queries), float(query_scale), B, H, Q,
+        C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()), int(workspace.numel()),
+        C.c_void_p(current_stream_ptr()),
+    )
+    _lib.check(st, "dc_decode_paged")
+    return out

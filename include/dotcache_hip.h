@@ -1,0 +1,222 @@
+/*
+ * dotcache_hip.h -- C ABI of the MI355X compressed-page decode-attention
+ * backend (libdotcache_hip.so, built for gfx950).
+ *
+ * All pointers marked (device) are HBM addresses; all sizes are in elements
+ * unless named *_bytes.  Every entry point returns 0 on success and a
+ * non-zero DC_E* status otherwise; dc_last_error() then returns a message.
+ * Host bindings map DC_EINVAL to ValueError and the other codes to
+ * RuntimeError, the error convention of the reference's backend surface
+ * (reference dotcache/attention_runtime.py:39-60).
+ *
+ * Work is enqueued on the given HIP stream (0 = default stream); nothing
+ * synchronises unless stated.  No entry point allocates device memory: the
+ * caller owns the page arena, descriptor tables, page tables, outputs and
+ * workspace.
+ *
+ * ---- page arena and page blobs --------------------------------------
+ * Pages live in one caller-owned byte arena.  A page blob starts at
+ * arena + 256 * desc.block and holds, for capacity C = geometry.page_capacity
+ * tokens (the token stride; desc.tokens <= C are valid):
+ *
+ *   M0 (affine / symmetric, b-bit codes, G groups, W = ceil(gs*b/32) words):
+ *     payload  uint32 [G][C][W]   group_major   (or [C][G][W] token_major)
+ *     scales   fp16   [C][G]      at align16(payload bytes)
+ *     bias     fp16   [C][G]      after scales (affine only)
+ *   M3 fp16 : fp16 [C][head_dim]
+ *   M3 fp32 : fp32 [C][head_dim]
+ *   M3 int8 : int8 [C][head_dim], then fp16 [C] row scales at align16
+ *
+ * which is the reference page contract: payload [G, T, W] uint32 packed
+ * little-endian (reference dotcache/packing.py:14-48,
+ * dotcache/page_format.py:19-23), scales / bias [T, G] fp16
+ * (reference dotcache/encode.py:427-428), escape rows [T, head_dim]
+ * (reference dotcache/modes/m3_escape.py:10-19).
+ */
+#ifndef DOTCACHE_HIP_H
+#define DOTCACHE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* dc_stream_t; /* a hipStream_t */
+
+enum dc_status {
+  DC_OK = 0,
+  DC_EINVAL = 1,   /* bad shape / mode / unsupported page  -> ValueError   */
+  DC_EDEVICE = 2,  /* HIP runtime failure                   -> RuntimeError */
+  DC_ESPACE = 3,   /* workspace or table too small          -> RuntimeError */
+};
+
+enum dc_page_format {
+  DC_FMT_M3_F16 = 0,       /* exact fp16 escape rows                      */
+  DC_FMT_M0_AFFINE = 1,    /* s * c + b                                   */
+  DC_FMT_M0_SYMMETRIC = 2, /* s * (c - (2^(b-1) - 1))                     */
+  DC_FMT_M3_F32 = 3,       /* fp32 escape rows                            */
+  DC_FMT_M3_I8 = 4,        /* int8 rows * fp16 row scale                  */
+};
+
+enum dc_dtype { DC_F32 = 0, DC_F16 = 1, DC_BF16 = 2 };
+
+/* One page: where its blob is and how to read it (8 bytes). */
+typedef struct dc_page_desc {
+  uint32_t block;  /* blob byte offset / 256                               */
+  uint16_t tokens; /* valid tokens (<= page_capacity)                      */
+  uint8_t format;  /* dc_page_format                                       */
+  uint8_t bits;    /* M0 code width: 2, 3, 4 or 8 (ignored for M3)         */
+} dc_page_desc;
+
+/* Geometry shared by every page of one call (one layer's pages). */
+typedef struct dc_page_geometry {
+  int32_t head_dim;
+  int32_t group_size;
+  int32_t page_capacity; /* token stride of a blob (tokens_per_page)        */
+  int32_t layout;        /* 0 = group_major, 1 = token_major                */
+} dc_page_geometry;
+
+/* A view of one page pool: the arena and its descriptor table.  Kernels
+ * skip (never read) a page whose id is outside [0, n_descs) or whose blob
+ * would end past arena_bytes; hosts validate tables before calling, this
+ * is a fault guard only. */
+typedef struct dc_pool {
+  void* arena;               /* device                                  */
+  int64_t arena_bytes;
+  const dc_page_desc* descs; /* device [n_descs]                        */
+  int32_t n_descs;
+  dc_page_geometry geometry;
+} dc_pool;
+
+/* One unit of decode work: pages [page_begin, page_end) of one
+ * (sequence, kv_head).  partial < 0: the item covers the whole sequence and
+ * writes the normalised output; otherwise it writes split-K partial
+ * (m, l, o) slot `partial`. */
+typedef struct dc_work_item {
+  int32_t seq;
+  int32_t kv_head;
+  int32_t page_begin;
+  int32_t page_end;
+  int32_t partial;
+  int32_t reserved[3];
+} dc_work_item;
+
+/* Log-sum-exp merge of partials [partial_begin, partial_begin + count) into
+ * the output of (seq, kv_head). */
+typedef struct dc_merge_item {
+  int32_t seq;
+  int32_t kv_head;
+  int32_t partial_begin;
+  int32_t count;
+} dc_merge_item;
+
+/* ---- library ---------------------------------------------------------- */
+
+/* Message for the last non-zero status returned on this thread. */
+const char* dc_last_error(void);
+
+/* ABI version (bumped on any signature or layout change). */
+int32_t dc_abi_version(void);
+
+/* Bytes of one page blob of the given format (host only, no GPU call).
+ * Replaces the byte accounting of reference dotcache/types.py:85-106 for
+ * device residency (EncodedPage.payload_nbytes + scales/bias). */
+int64_t dc_page_blob_bytes(int32_t format, int32_t bits, dc_page_geometry geometry);
+
+/* Compressed bytes a reader fetches for `tokens` valid tokens of a page
+ * (codes + fp16 scales/bias, or escape rows): the roofline's
+ * algorithmic-bytes figure.  Host only. */
+int64_t dc_page_read_bytes(int32_t format, int32_t bits, int32_t tokens, dc_page_geometry geometry);
+
+/* ---- write path ------------------------------------------------------- */
+
+/* Encode rows values[r, :head_dim] (dtype DC_F32/F16/BF16, row stride
+ * `row_stride` elements) into token slot row_slot[r] of page
+ * row_page[r] of the arena, using that page's format.  M0 scales and
+ * codes are per (token, group), so encoding a page row by row is
+ * bit-identical to encoding it whole; this one entry point is both the page
+ * encoder and the per-step append of a new token.  Does not change
+ * desc.tokens (the caller owns page fill counts).
+ * Replaces reference dotcache/encode.py:122-445 (encode_page, M0 and M3
+ * branches) with dotcache/modes/m0_affine.py:15-53 and
+ * dotcache/packing.py:14-48, and the tail append of
+ * dotcache/model_kv_cache.py:3830-4025.  Bit-exact with them. */
+int dc_encode_rows(const void* values, int32_t values_dtype, int64_t n_rows, int64_t row_stride,
+                   const int32_t* row_page /* device [n_rows] */,
+                   const int32_t* row_slot /* device [n_rows] */,
+                   dc_pool pool, dc_stream_t stream);
+
+/* ---- read path: per-page entry points (score_page / mix_page) ------- */
+
+/* logits[q, token_offsets[i] + t] = score of query q against token t of
+ * page page_ids[i], for n_queries fp32 queries [n_queries, head_dim].
+ * token_offsets (device, [n_pages + 1]) is the prefix sum of page token
+ * counts.  Replaces reference dotcache/attention_reference.py:34-128
+ * (score_page_ref) behind dotcache/backends/torch_cuda.py:53-68
+ * (score_page_cuda / score_pages_cuda). */
+int dc_score_pages(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets, int32_t n_pages,
+                   const float* queries, int32_t n_queries, float* logits, int64_t logits_stride,
+                   dc_stream_t stream);
+
+/* out[q, :head_dim] (+)= sum_i weights[q, token_offsets[i] + t] * V(page_ids[i])[t, :].
+ * accumulate != 0 adds into out (the out_acc of the reference).  Replaces
+ * reference dotcache/attention_reference.py:131-194 (mix_page_ref) behind
+ * dotcache/backends/torch_cuda.py:71-78 (mix_page_cuda). */
+int dc_mix_pages(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets, int32_t n_pages,
+                 const float* weights, int32_t n_queries, int64_t weights_stride, float* out,
+                 int32_t accumulate, dc_stream_t stream);
+
+/* In-place row softmax exp(x - max) / sum of x[r, :n_cols] (row stride
+ * `stride`), the global softmax of reference
+ * dotcache/attention_reference.py:27-31 used by the decode_step entry
+ * point that returns logits and weights. */
+int dc_softmax_rows(float* x /* device */, int32_t n_rows, int32_t n_cols, int64_t stride, dc_stream_t stream);
+
+/* ---- read path: fused paged decode ------------------------------------ */
+
+/* Host-only planner: split each (sequence, kv_head)'s page list into work
+ * items of at most pages_per_split pages (pages_per_split <= 0: one item
+ * per sequence), and emit merge items for sequences that were split.
+ * seq_pages: host [n_seqs].  Returns DC_ESPACE if the output arrays are too
+ * small (counts are still written). */
+int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t pages_per_split,
+                   dc_work_item* items, int32_t max_items, int32_t* n_items,
+                   dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials);
+
+/* Fused decode attention straight from compressed pages: for every work
+ * item, score its pages for the n_q GQA query heads of its KV head, take a
+ * single-pass online softmax, and mix the value pages; then merge split-K
+ * partials by log-sum-exp.  Pages of one item may mix formats (per-page
+ * M3 / M0, the selective-key-precision map).
+ *   queries : device [n_seqs, n_kv_heads, n_q, head_dim] of queries_dtype
+ *             (= [n_seqs, n_q_heads, head_dim] with q_head -> q_head / n_q,
+ *             reference dotcache/model_kv_cache.py:85-95), multiplied by
+ *             query_scale before use
+ *   k_pool, v_pool : pools of the key and value pages; they must share
+ *             head_dim and page_capacity and may differ in group size
+ *             (one group size per pool); they may be the same pool
+ *   k_table, v_table : device int32 [n_seqs, n_kv_heads, table_stride] page
+ *             ids into k_pool / v_pool
+ *   out     : device fp32 [n_seqs, n_kv_heads, n_q, head_dim]
+ *   workspace : device, >= dc_decode_workspace_bytes(n_partials, n_q, head_dim)
+ * Replaces reference dotcache/attention_runtime.py:179-315 (decode_step,
+ * decode_multi_query_step) and the grouped GPU decode of
+ * dotcache/backends/torch_mps.py:4110-4435 behind
+ * dotcache/backends/torch_cuda.py:81-158. */
+int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table, int32_t table_stride,
+                    const dc_work_item* items, int32_t n_items,
+                    const dc_merge_item* merges, int32_t n_merges,
+                    const void* queries, int32_t queries_dtype, float query_scale,
+                    int32_t n_seqs, int32_t n_kv_heads, int32_t n_q,
+                    float* out, void* workspace, int64_t workspace_bytes,
+                    dc_stream_t stream);
+
+int64_t dc_decode_workspace_bytes(int32_t n_partials, int32_t n_q, int32_t head_dim);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOTCACHE_HIP_H */

@@ -1,0 +1,91 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol that
+include/dotcache_hip.h declares, and its host-only entry points (blob sizes,
+read-byte accounting, decode planner) give the right answers.  No GPU call."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from dotcache_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "dotcache_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dc_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = _declared()
+    assert "dc_decode_paged" in names and "dc_encode_rows" in names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_abi_version():
+    assert _lib.lib().dc_abi_version() == 1
+
+
+def test_blob_bytes_match_layout():
+    g = _lib.geometry(128, 32, 64)
+    # M0 sym 4-bit: codes 4*64*4*4 = 4096, scales 64*4*2 = 512 -> 4608 (a multiple of 256)
+    assert _lib.page_blob_bytes(_lib.FMT_M0_SYMMETRIC, 4, g) == 4608
+    assert _lib.page_blob_bytes(_lib.FMT_M0_AFFINE, 4, g) == 4096 + 512 + 512 + 0  # 5120, already aligned
+    assert _lib.page_blob_bytes(_lib.FMT_M3_F16, 0, g) == 16384
+    with pytest.raises(ValueError):
+        _lib.page_blob_bytes(_lib.FMT_M0_AFFINE, 5, g)
+
+
+def test_read_bytes_are_algorithmic_bytes():
+    g = _lib.geometry(128, 32, 64)
+    assert _lib.page_read_bytes(_lib.FMT_M3_F16, 0, 64, g) == 16384
+    assert _lib.page_read_bytes(_lib.FMT_M0_SYMMETRIC, 4, 64, g) == 4608
+    assert _lib.page_read_bytes(_lib.FMT_M0_AFFINE, 4, 10, g) == 10 * (64 + 16)
+    g64 = _lib.geometry(128, 64, 64)
+    assert _lib.page_read_bytes(_lib.FMT_M0_SYMMETRIC, 8, 64, g64) == 64 * (128 + 4)  # C4 V: 132 B/token
+
+
+def _plan(seq_pages, heads, per):
+    sp = np.asarray(seq_pages, dtype=np.int32)
+    L = _lib.lib()
+    ni, nm, npart = C.c_int32(), C.c_int32(), C.c_int32()
+    items = (_lib.WorkItem * 256)()
+    merges = (_lib.MergeItem * 256)()
+    st = L.dc_plan_decode(sp.ctypes.data, sp.size, heads, per, C.addressof(items), 256, C.byref(ni),
+                          C.addressof(merges), 256, C.byref(nm), C.byref(npart))
+    _lib.check(st, "plan")
+    its = [(i.seq, i.kv_head, i.page_begin, i.page_end, i.partial) for i in items[: ni.value]]
+    ms = [(m.seq, m.kv_head, m.partial_begin, m.count) for m in merges[: nm.value]]
+    return its, ms, npart.value
+
+
+def test_planner_covers_every_page_once():
+    its, ms, npart = _plan([5, 1, 9], 2, 4)
+    for b, n in enumerate([5, 1, 9]):
+        for h in range(2):
+            covered = sorted(p for (s, hh, pb, pe, _) in its if s == b and hh == h for p in range(pb, pe))
+            assert covered == list(range(n))
+    # sequence 1 (one page) is not split: it writes the output directly
+    assert all(part == -1 for (s, _, _, _, part) in its if s == 1)
+    assert npart == 2 * (2 + 3)
+    assert sorted(ms) == [(0, 0, 0, 2), (0, 1, 2, 2), (2, 0, 4, 3), (2, 1, 7, 3)]
+
+
+def test_planner_rejects_empty_sequence():
+    with pytest.raises(ValueError):
+        _plan([3, 0], 1, 2)
+
+
+def test_planner_reports_short_tables():
+    sp = np.asarray([100], dtype=np.int32)
+    ni, nm, npart = C.c_int32(), C.c_int32(), C.c_int32()
+    items = (_lib.WorkItem * 2)()
+    st = _lib.lib().dc_plan_decode(sp.ctypes.data, 1, 1, 10, C.addressof(items), 2, C.byref(ni), None, 0,
+                                   C.byref(nm), C.byref(npart))
+    assert st == _lib.DC_ESPACE and ni.value == 10 and nm.value == 1

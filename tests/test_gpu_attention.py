@@ -1,0 +1,125 @@
+"""GPU read-path parity against the oracle: score_page / mix_page /
+decode_step through the backend surface, and the fused paged decode
+(GQA, split-K, ragged batches, mixed per-page formats)."""
+import numpy as np
+import pytest
+
+from oracle import dotcache_oracle as O
+from tests.helpers import hard_values, to_product_page
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [
+    dict(mode="M0", scheme="affine", bits=4),
+    dict(mode="M0", scheme="symmetric", bits=4),
+    dict(mode="M0", scheme="symmetric", bits=8),
+    dict(mode="M0", scheme="affine", bits=2),
+    dict(mode="M0", scheme="affine", bits=3),
+    dict(mode="M3", scheme="affine", bits=4),
+    dict(mode="M3", scheme="affine", bits=4, escape_dtype="int8"),
+]
+
+
+def _pages(x, tpp, hd, gs, kind, fmt):
+    return O.encode_pages(x, tokens_per_page=tpp, head_dim=hd, group_size=gs, kind=kind, **fmt)
+
+
+@pytest.mark.parametrize("fmt", FORMATS, ids=lambda f: "-".join(str(v) for v in f.values()))
+def test_score_and_mix_page_match_oracle(fmt):
+    from dotcache_amd import attention_runtime as rt
+
+    rng = np.random.default_rng(901)
+    hd, gs = 128, 32
+    k = hard_values(rng, 64, hd)
+    q = rng.normal(size=hd).astype(np.float32)
+    page = O.encode_page(k, head_dim=hd, group_size=gs, kind="K", **fmt)
+    got = rt.score_page(q, to_product_page(page), backend="hip_mi355x")
+    np.testing.assert_allclose(got, O.score_page_ref(q, page), atol=1e-4, rtol=1e-4)
+    w = O.softmax(rng.normal(size=64).astype(np.float32))
+    acc = rng.normal(size=hd).astype(np.float32)
+    got_mix = rt.mix_page(w, to_product_page(page), out_acc=acc, backend="hip_mi355x")
+    np.testing.assert_allclose(got_mix, acc + O.mix_page_ref(w, page), atol=1e-4, rtol=1e-4)
+
+
+def test_decode_step_matches_cpu_reference():
+    """Reference tests/test_torch_cuda_backend.py:53-79 shape: hd 128, 160 tokens."""
+    from dotcache_amd import attention_runtime as rt
+
+    rng = np.random.default_rng(902)
+    hd = 128
+    keys = rng.normal(size=(160, hd)).astype(np.float32)
+    values = rng.normal(size=(160, hd)).astype(np.float32)
+    q = rng.normal(size=hd).astype(np.float32)
+    kp = _pages(keys, 64, hd, 32, "K", dict(bits=4))
+    vp = _pages(values, 64, hd, 32, "V", dict(bits=4))
+    want = O.decode_step(q, kp, vp)
+    got = rt.decode_step(q, [to_product_page(p) for p in kp], [to_product_page(p) for p in vp], backend="hip_mi355x")
+    np.testing.assert_allclose(got[0], want[0], atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(got[1], want[1], atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(got[2], want[2], atol=1e-4, rtol=1e-4)
+
+
+def test_score_pages_splits_per_page():
+    from dotcache_amd.backends import score_pages_hip
+
+    rng = np.random.default_rng(903)
+    keys = rng.normal(size=(150, 64)).astype(np.float32)
+    q = rng.normal(size=64).astype(np.float32)
+    kp = _pages(keys, 64, 64, 32, "K", dict(bits=4))
+    got = score_pages_hip(q, [to_product_page(p) for p in kp])
+    assert [g.shape[0] for g in got] == [64, 64, 22]
+    for g, p in zip(got, kp):
+        np.testing.assert_allclose(g, O.score_page_ref(q, p), atol=1e-4, rtol=1e-4)
+
+
+def _grouped_case(rng, hd, gs, Q, n_tokens, kfmt, vfmt, tpp=64):
+    G = len(n_tokens)
+    qs = rng.normal(size=(G, Q, hd)).astype(np.float32)
+    kpg, vpg = [], []
+    for n in n_tokens:
+        kpg.append(_pages(hard_values(rng, n, hd), tpp, hd, gs, "K", kfmt))
+        vpg.append(_pages(hard_values(rng, n, hd), tpp, hd, gs, "V", vfmt))
+    return qs, kpg, vpg
+
+
+@pytest.mark.parametrize("kfmt,vfmt,hd,gs,Q", [
+    (dict(mode="M3"), dict(bits=4, scheme="symmetric"), 128, 32, 7),           # C3 formats
+    (dict(bits=4), dict(bits=4), 64, 32, 4),                                    # C2 formats
+    (dict(bits=4), dict(bits=8, scheme="symmetric"), 128, 64, 6),               # C4 V format (g64)
+    (dict(bits=4), dict(bits=4), 256, 32, 4),                                   # C5 formats
+    (dict(bits=2), dict(bits=3), 128, 32, 3),
+    (dict(mode="M3", escape_dtype="int8"), dict(mode="M3", escape_dtype="float32"), 64, 32, 16),
+])
+def test_fused_output_only_matches_oracle(kfmt, vfmt, hd, gs, Q):
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+
+    rng = np.random.default_rng(hd + Q)
+    qs, kpg, vpg = _grouped_case(rng, hd, gs, Q, [1000, 64, 130], kfmt, vfmt)
+    qs = qs / np.sqrt(hd)
+    want = O.decode_grouped(qs, kpg, vpg)
+    kp = [[to_product_page(p) for p in g] for g in kpg]
+    vp = [[to_product_page(p) for p in g] for g in vpg]
+    for pps in (None, 1, 3):
+        got = fused(list(qs), kp, vp, pages_per_split=pps).cpu().numpy()
+        np.testing.assert_allclose(got, want, atol=1e-3, rtol=0)
+        assert np.max(np.abs(got - want)) < 2e-4
+
+
+def test_fused_mixed_key_formats_per_page():
+    """Selective key precision: M3 and M0 key pages interleaved in one list."""
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+    from dotcache_amd.types import EncodedPage
+
+    rng = np.random.default_rng(77)
+    hd, n = 128, 640
+    keys = hard_values(rng, n, hd)
+    vals = hard_values(rng, n, hd)
+    kp = []
+    for i, s in enumerate(range(0, n, 64)):
+        fmt = dict(mode="M3") if i % 3 == 1 else dict(bits=4, scheme="affine")
+        kp.append(O.encode_page(keys[s:s + 64], head_dim=hd, group_size=32, kind="K", token_start=s, **fmt))
+    vp = _pages(vals, 64, hd, 64, "V", dict(bits=8, scheme="symmetric"))  # V group 64, K group 32 (config 4)
+    q = (rng.normal(size=(1, 6, hd)) / np.sqrt(hd)).astype(np.float32)
+    want = O.decode_grouped(q, [kp], [vp])
+    got = fused(list(q), [[to_product_page(p) for p in kp]], [[to_product_page(p) for p in vp]]).cpu().numpy()
+    np.testing.assert_allclose(got, want, atol=2e-4, rtol=0)
