@@ -1,0 +1,218 @@
+"""Decode-attention throughput on compressed KV pages (one MI355X).
+
+A step is one decode step of the whole model: for every layer, one fused
+``dc_decode_paged`` launch over the whole batch (plus, for workloads with
+append, the encode/append of the new token).  Inputs are resident in HBM
+before timing starts.  Prints ONE JSON line on stdout; progress goes to
+stderr.
+
+    python bench.py [--steps K] [--warmup W] [--config c3] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "KV tokens attended/s + HBM GB/s (% of 8 TB/s peak), 7B GQA, 16K ctx, batch 8"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--pages-per-split", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def cpu_baseline(wl, budget_s: float) -> dict:
+    """Time the CPU oracle (numpy restatement of the reference cpu_ref path)
+    on a bounded sample of the same workload: layer 0, sequence 0, all KV
+    heads, as many GQA query heads as fit in ``budget_s``.  One (sequence,
+    layer, token) position covers every query head, so the rate is
+    tokens x (query heads done / query heads) / seconds."""
+    from threadpoolctl import threadpool_limits
+
+    from dotcache_amd.types import PageHeader
+    from oracle import dotcache_oracle as O
+
+    spec = wl.spec
+    lt = wl.layers[0]
+    n = int(lt.seq_pages[0])
+    kt = lt.k_table[0].cpu().numpy()
+    vt = lt.v_table[0].cpu().numpy()
+    q_all = wl.queries[0][0].float().cpu().numpy() * wl.query_scale  # [H, Q, hd]
+
+    def hdr(kind, geo, fmt, bits, T):
+        from dotcache_amd import _lib
+        mode = "M3" if fmt == _lib.FMT_M3_F16 else "M0"
+        scheme = "symmetric" if fmt == _lib.FMT_M0_SYMMETRIC else "affine"
+        G = -(-geo.head_dim // geo.group_size)
+        b = bits if mode == "M0" else 4
+        return PageHeader(layer_id=0, kv_head_id=0, kind=kind, token_start=0, token_count=T, head_dim=geo.head_dim,
+                          padded_head_dim=G * geo.group_size, group_size=geo.group_size, num_groups=G, bits=b,
+                          words_per_group=(geo.group_size * b + 31) // 32, mode_default=mode, layout="group_major",
+                          quant_scheme=scheme)
+
+    def to_oracle(pool, pid, kind):
+        d = pool.desc(pid)
+        page = pool.download_page(int(pid), hdr(kind, pool.geometry, int(d["format"]), int(d["bits"]), int(d["tokens"])))
+        oh = O.OracleHeader(**page.header.to_dict())
+        return O.OraclePage(header=oh, payload=page.payload, scales=page.scales, bias=page.bias,
+                            escape_payload=page.escape_payload, escape_scales=page.escape_scales)
+
+    H, Q = spec.n_kv_heads, spec.gqa
+    kp = [[to_oracle(wl.k_pool, kt[h, p], "K") for p in range(n)] for h in range(H)]
+    vp = [[to_oracle(wl.v_pool, vt[h, p], "V") for p in range(n)] for h in range(H)]
+    tokens = int(sum(p.header.token_count for p in kp[0]))
+    done = 0
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        for j in range(Q):
+            for h in range(H):
+                O.decode_step(q_all[h, j], kp[h], vp[h])
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        dt = time.perf_counter() - t0
+    rate = tokens * done / Q / dt
+    return {
+        "value": rate,
+        "unit": "KV tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"layer 0, sequence 0, {H} KV heads x {done}/{Q} query heads over {tokens} tokens "
+                  f"({n} pages) in {dt:.1f} s; numpy oracle of reference cpu_ref (BLAS pinned to 1 thread); "
+                  f"host {os.cpu_count()} cpus",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU). "
+              "The path shards by (sequence, KV head) with no exchange, see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from dotcache_amd.workloads import SPECS, build_workload
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    t0 = time.time()
+    log(f"building workload {args.config} ...")
+    wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split)
+    spec = wl.spec
+    log(f"built in {time.time() - t0:.1f} s: {wl.plan.n_items} work items/layer, pages/split {wl.plan.pages_per_split}, "
+        f"K pool {wl.k_pool.arena.numel() / 1e9:.2f} GB, V pool {wl.v_pool.arena.numel() / 1e9:.2f} GB")
+
+    for _ in range(args.warmup):
+        wl.step()
+    torch.cuda.synchronize()
+
+    L = spec.n_layers
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
+          for _ in range(args.steps)]
+    cur = {"s": 0}
+
+    def hook(l, what):
+        e = ev[cur["s"]][l][0 if what == "begin" else 1]
+        e.record()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for s in range(args.steps):
+        cur["s"] = s
+        wl.step(layer_hook=hook)
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_step = total_ms / args.steps
+    layer_ms = np.array([[b.elapsed_time(e) for (b, e) in row] for row in ev])
+    launch_ms = float(layer_ms.mean())
+
+    bytes_step = wl.algorithmic_bytes_per_step()
+    pos_step = wl.token_positions_per_step()
+    value = pos_step / (ms_step / 1e3)
+    gbps = bytes_step / (ms_step / 1e3) / 1e9
+    bytes_launch = bytes_step / L
+    achieved = bytes_launch / (launch_ms / 1e3) / 1e9
+    log(f"{ms_step:.3f} ms/step, {value / 1e9:.3f} G tokens/s, {gbps:.0f} GB/s over the step; "
+        f"decode launch {launch_ms * 1e3:.1f} us -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle baseline ...")
+        cpu = cpu_baseline(wl, args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']:.0f} tokens/s ({cpu['sample']})")
+
+    fmt = lambda f: f"{f.mode} fp16" if f.mode == "M3" else f"M0 {f.scheme} int{f.bits} g{f.group_size}"
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "KV tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded; K/V encoded on device into compressed pages)",
+        "config": {
+            "workload": spec.name,
+            "layers": L,
+            "batch": spec.batch,
+            "context": int(spec.context) if spec.ragged is None else f"log-uniform {spec.ragged}",
+            "q_heads": spec.n_q_heads,
+            "kv_heads": spec.n_kv_heads,
+            "head_dim": spec.head_dim,
+            "page_size": spec.page_size,
+            "key_pages": fmt(spec.key) + (f", {spec.key_m3_fraction:.0%} streams M3" if spec.key_m3_fraction else ""),
+            "value_pages": fmt(spec.value),
+            "append": spec.append,
+            "pages_per_split": wl.plan.pages_per_split,
+            "parallelism": "single GPU",
+        },
+        "hbm_gbps": gbps,
+        "hbm_pct_of_peak": 100.0 * gbps / HBM_PEAK_GBPS,
+        "bytes_per_step": bytes_step,
+        "token_positions_per_step": pos_step,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": None,
+            "kernel": "dc_decode_paged (per-layer launch)",
+            "launch_us": launch_ms * 1e3,
+            "bytes_per_launch": bytes_launch,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

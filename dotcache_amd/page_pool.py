@@ -179,8 +179,8 @@ class DevicePagePool:
         self._dirty = True
 
     def set_tokens(self, page_ids, tokens) -> None:
-        ids = np.atleast_1d(np.asarray(page_ids, dtype=np.int64))
-        tok = np.broadcast_to(np.asarray(tokens, dtype=np.int64), ids.shape)
+        ids = np.atleast_1d(np.asarray(page_ids, dtype=np.int64)).ravel()
+        tok = np.broadcast_to(np.asarray(tokens, dtype=np.int64).ravel() if np.ndim(tokens) else tokens, ids.shape)
         if np.any(tok < 0) or np.any(tok > self.geometry.page_capacity):
             raise ValueError("token count outside [0, page_capacity]")
         self._host_desc["tokens"][ids] = tok
