@@ -30,7 +30,13 @@ class Pool(C.Structure):
         ("descs", C.c_void_p),
         ("n_descs", C.c_int32),
         ("geometry", PageGeometry),
+        ("format_mask", C.c_uint64),
     ]
+
+
+def format_bit(fmt: int, bits: int) -> int:
+    """Bit of a page format in dc_pool.format_mask (format * 9 + bits, bits 0 for M3)."""
+    return 1 << (int(fmt) * 9 + (0 if fmt in (FMT_M3_F16, FMT_M3_F32, FMT_M3_I8) else int(bits)))
 
 
 class WorkItem(C.Structure):
@@ -63,6 +69,7 @@ SIGNATURES = {
                                   C.c_void_p, C.c_int32, C.c_float, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                   C.c_void_p, C.c_int64, C.c_void_p]),
     "dc_decode_workspace_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32]),
+    "dc_set_decode_path": (C.c_int, [C.c_int32]),
 }
 
 _lib: C.CDLL | None = None

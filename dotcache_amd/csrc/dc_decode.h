@@ -42,6 +42,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 int launch_decode(const DecodeArgs& a, hipStream_t stream);
 int launch_decode_generic(const DecodeArgs& a, hipStream_t stream);
+// Launches the MFMA kernel when every format in the pools' masks and the
+// geometry fit it; *launched tells the caller whether to fall back.
+int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched);
 int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream);
 
 }  // namespace dc

@@ -221,7 +221,14 @@ int launch_decode_generic(const DecodeArgs& a, hipStream_t stream) {
   return check_hip(hipGetLastError(), "decode_generic_kernel launch");
 }
 
-int launch_decode(const DecodeArgs& a, hipStream_t stream) { return launch_decode_generic(a, stream); }
+static int g_decode_path = 0;  // 0 = fastest kernel that fits, 1 = generic kernel only
+
+int launch_decode(const DecodeArgs& a, hipStream_t stream) {
+  bool launched = false;
+  if (g_decode_path == 0)
+    if (int rc = launch_decode_mfma(a, stream, &launched)) return rc;
+  return launched ? DC_OK : launch_decode_generic(a, stream);
+}
 
 int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream) {
   if (n_merges <= 0) return DC_OK;
@@ -246,6 +253,8 @@ extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_
     return dc::fail(DC_EINVAL, "dc_decode_paged: bad counts");
   if (n_q <= 0 || n_q > dc::kMaxQ) return dc::fail(DC_EINVAL, "n_q must be in [1, %d]", dc::kMaxQ);
   if (g.head_dim > dc::kMaxHD) return dc::fail(DC_EINVAL, "head_dim %d exceeds %d", g.head_dim, dc::kMaxHD);
+  if (dc::num_groups(g) * g.group_size > dc::kMaxHD)
+    return dc::fail(DC_EINVAL, "padded head_dim %d exceeds %d", dc::num_groups(g) * g.group_size, dc::kMaxHD);
   if (dc::num_groups(g) > dc::kMaxGroups || dc::num_groups(v_pool.geometry) > dc::kMaxGroups) return dc::fail(DC_EINVAL, "more than %d groups per head", dc::kMaxGroups);
   if (g.page_capacity > dc::kMaxCap)
     return dc::fail(DC_EINVAL, "page_capacity %d exceeds %d for decode", g.page_capacity, dc::kMaxCap);
@@ -284,4 +293,10 @@ extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_
   int rc = dc::launch_decode(a, hipStream_t(stream));
   if (rc) return rc;
   return dc::launch_merge(a, merges, n_merges, hipStream_t(stream));
+}
+
+extern "C" int dc_set_decode_path(int32_t path) {
+  if (path != 0 && path != 1) return dc::fail(DC_EINVAL, "decode path must be 0 (auto) or 1 (generic)");
+  dc::g_decode_path = path;
+  return DC_OK;
 }

@@ -20,10 +20,12 @@ import numpy as np
 from . import _lib
 from .page_pool import DevicePagePool, current_stream_ptr, dtype_code
 
-# Split long page lists so a launch has enough work items to fill the
-# 256 CUs, but keep each item long enough to amortise its setup.
-DEFAULT_TARGET_ITEMS = 2048
-MIN_PAGES_PER_SPLIT = 8
+# Split long page lists so a launch has about two workgroups (of four
+# wavefronts) per CU for the 256 CUs, but keep each item long enough that every
+# wavefront walks a few pages and the split-K partials stay a small fraction
+# of the bytes read.
+DEFAULT_TARGET_ITEMS = 512
+MIN_PAGES_PER_SPLIT = 4
 
 
 def _torch():
@@ -83,6 +85,13 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
         _plan_cache.clear()
     _plan_cache[key] = plan
     return plan
+
+
+def set_decode_path(path: str) -> None:
+    """``"auto"`` (MFMA kernel when the pages fit it) or ``"generic"``."""
+    if path not in ("auto", "generic"):
+        raise ValueError("decode path must be 'auto' or 'generic'")
+    _lib.check(_lib.lib().dc_set_decode_path(0 if path == "auto" else 1), "dc_set_decode_path")
 
 
 def workspace_bytes(plan: DecodePlan, n_q: int, head_dim: int) -> int:

@@ -101,7 +101,9 @@ class DevicePagePool:
             raise ValueError("page_capacity exceeds 65535")
         self.geometry = geometry
         self.device = torch.device(device)
-        self.arena = torch.empty(max(int(reserve_bytes), 256), dtype=torch.uint8, device=self.device)
+        # zero-filled so never-written token slots of a partial page hold finite values
+        self.arena = torch.zeros(max(int(reserve_bytes), 256), dtype=torch.uint8, device=self.device)
+        self.format_mask = 0
         self._next_block = 0
         self._free: dict[int, list[int]] = {}
         self._host_desc = np.zeros(max(int(reserve_pages), 16), dtype=DESC_DTYPE)
@@ -125,7 +127,7 @@ class DevicePagePool:
         if need <= self.arena.numel():
             return
         torch = _torch()
-        new = torch.empty(max(need, 2 * self.arena.numel()), dtype=torch.uint8, device=self.device)
+        new = torch.zeros(max(need, 2 * self.arena.numel()), dtype=torch.uint8, device=self.device)
         used = self._next_block * 256
         if used:
             new[:used].copy_(self.arena[:used])
@@ -160,6 +162,7 @@ class DevicePagePool:
                 self._next_block += nblk
             pid = self._new_id()
             self._host_desc[pid] = (block, tokens, fmt, bits)
+            self.format_mask |= _lib.format_bit(fmt, bits)
             self._live[pid] = True
             self._blob_size[pid] = nblk
             ids[i] = pid
@@ -214,7 +217,7 @@ class DevicePagePool:
         descs = self.device_descs()
         return _lib.Pool(
             C.c_void_p(self.arena.data_ptr()), self.arena.numel(), C.c_void_p(descs.data_ptr()), self._n_pages,
-            self.geometry.c(),
+            self.geometry.c(), self.format_mask,
         )
 
     # ---- host <-> device pages --------------------------------------------
@@ -283,6 +286,7 @@ class DevicePagePool:
             for j, i in enumerate(idx):
                 pid = self._new_id()
                 self._host_desc[pid] = (start + j * nblk, pages[i].header.token_count, fmt, bits)
+                self.format_mask |= _lib.format_bit(fmt, bits)
                 self._live[pid] = True
                 self._blob_size[pid] = nblk
                 self.headers[pid] = PageHeader.from_dict(pages[i].header.to_dict())

@@ -88,6 +88,10 @@ typedef struct dc_pool {
   const dc_page_desc* descs; /* device [n_descs]                        */
   int32_t n_descs;
   dc_page_geometry geometry;
+  /* bit (format * 9 + bits) is set for every page format the pool may
+   * hold (bits = 0 for M3); decode picks its kernel from this set, so a
+   * page whose format is not in the mask must not be in the pool */
+  uint64_t format_mask;
 } dc_pool;
 
 /* One unit of decode work: pages [page_begin, page_end) of one
@@ -214,6 +218,12 @@ int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, cons
                     dc_stream_t stream);
 
 int64_t dc_decode_workspace_bytes(int32_t n_partials, int32_t n_q, int32_t head_dim);
+
+/* Process-wide decode kernel choice: 0 (default) runs the MFMA kernel when
+ * every page format, head_dim (64/128/256), group size and n_q <= 8 fit it
+ * and the generic kernel otherwise; 1 always runs the generic kernel (for
+ * cross-checking the two).  Host only; not thread-safe. */
+int dc_set_decode_path(int32_t path);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,21 @@ from tests.helpers import hard_values, to_product_page
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True)
+def fresh_pools():
+    """Every test prepares into fresh pools, so the formats one test puts in a
+    pool never change which decode kernel another test gets."""
+    from dotcache_amd.backends import clear_prepared_pools
+    from dotcache_amd.decode import set_decode_path
+
+    clear_prepared_pools()
+    set_decode_path("auto")
+    yield
+    set_decode_path("auto")
+    clear_prepared_pools()
+
+
 FORMATS = [
     dict(mode="M0", scheme="affine", bits=4),
     dict(mode="M0", scheme="symmetric", bits=4),
@@ -123,3 +138,57 @@ def test_fused_mixed_key_formats_per_page():
     want = O.decode_grouped(q, [kp], [vp])
     got = fused(list(q), [[to_product_page(p) for p in kp]], [[to_product_page(p) for p in vp]]).cpu().numpy()
     np.testing.assert_allclose(got, want, atol=2e-4, rtol=0)
+
+
+FAST_CASES = [
+    # (key format, value format, head_dim, value group, n_q, page tokens): every BASELINE shape
+    (dict(mode="M3"), dict(bits=4, scheme="symmetric"), 128, 32, 7, 64),          # config 3
+    (dict(bits=4), dict(bits=4), 64, 32, 4, 64),                                   # config 2
+    (dict(bits=4, scheme="symmetric"), dict(bits=4, scheme="symmetric"), 64, 32, 1, 64),  # config 1
+    (dict(bits=4), dict(bits=8, scheme="symmetric"), 128, 64, 6, 64),              # config 4
+    (dict(bits=4), dict(bits=4), 256, 32, 4, 128),                                 # config 5
+    (dict(mode="M3"), dict(mode="M3"), 128, 32, 8, 64),
+    (dict(bits=4, scheme="symmetric"), dict(bits=8), 128, 32, 5, 96),
+]
+
+
+@pytest.mark.parametrize("path", ["auto", "generic"])
+@pytest.mark.parametrize("kfmt,vfmt,hd,vgs,Q,tpp", FAST_CASES)
+def test_fused_kernels_match_oracle(kfmt, vfmt, hd, vgs, Q, tpp, path):
+    """The MFMA kernel (auto) and the generic kernel on the same pages, with
+    ragged groups, partial last pages, outlier channels and split-K."""
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+    from dotcache_amd.decode import set_decode_path
+
+    set_decode_path(path)
+    rng = np.random.default_rng(hd * 7 + Q + tpp)
+    lens = [tpp * 5 + 17, 1, tpp - 3, 3 * tpp]
+    G = len(lens)
+    qs = (rng.normal(size=(G, Q, hd)) / np.sqrt(hd)).astype(np.float32)
+    kpg = [_pages(hard_values(rng, n, hd), tpp, hd, 32, "K", kfmt) for n in lens]
+    vpg = [_pages(hard_values(rng, n, hd), tpp, hd, vgs, "V", vfmt) for n in lens]
+    want = O.decode_grouped(qs, kpg, vpg)
+    kp = [[to_product_page(p) for p in g] for g in kpg]
+    vp = [[to_product_page(p) for p in g] for g in vpg]
+    for pps in (None, 2):
+        got = fused(list(qs), kp, vp, pages_per_split=pps).cpu().numpy()
+        err = np.max(np.abs(got - want))
+        assert err < 2e-4, f"path {path} pps {pps}: max-abs error {err}"
+
+
+def test_fused_decode_peaked_attention_and_small_values():
+    """Sharp softmax (a few tokens dominate) and tiny value scales: the fp16
+    high/residual split of weight x scale must keep the error below 1e-3."""
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+
+    rng = np.random.default_rng(5)
+    hd, n, Q = 128, 2000, 7
+    k = rng.normal(size=(n, hd)).astype(np.float32)
+    v = (rng.normal(size=(n, hd)) * 1e-3).astype(np.float32)
+    v[::97] *= 5e4  # a few large rows
+    q = rng.normal(size=(1, Q, hd)).astype(np.float32) * 0.6  # logits spread ~ +-20
+    kp = _pages(k, 64, hd, 32, "K", dict(mode="M3"))
+    vp = _pages(v, 64, hd, 32, "V", dict(bits=4, scheme="symmetric"))
+    want = O.decode_grouped(q, [kp], [vp])
+    got = fused(list(q), [[to_product_page(p) for p in kp]], [[to_product_page(p) for p in vp]]).cpu().numpy()
+    assert np.max(np.abs(got - want)) < 1e-3
