@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--pages-per-split", type=int, default=None)
+    ap.add_argument("--contiguous-pages", action="store_true",
+                    help="keep each sequence's pages in allocation order instead of scattering them over the pool")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     return ap.parse_args()
@@ -119,7 +121,8 @@ def main():
     torch.cuda.set_device(0)
     t0 = time.time()
     log(f"building workload {args.config} ...")
-    wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split)
+    wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
+                        scatter_pages=not args.contiguous_pages)
     spec = wl.spec
     log(f"built in {time.time() - t0:.1f} s: {wl.plan.n_items} work items/layer, pages/split {wl.plan.pages_per_split}, "
         f"K pool {wl.k_pool.arena.numel() / 1e9:.2f} GB, V pool {wl.v_pool.arena.numel() / 1e9:.2f} GB")

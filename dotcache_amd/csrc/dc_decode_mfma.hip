@@ -75,57 +75,78 @@ __device__ __forceinline__ uint32_t h2_const(float v) { return pack_h2(v, v); }
 // fp16 bits (low 16 bits of x) -> float
 __device__ __forceinline__ float h2f(uint32_t x) { return float(__builtin_bit_cast(_Float16, uint16_t(x))); }
 
+// Two fp32 values as packed fp16: their high parts rtz(x) (res_neg = 0) or
+// their residuals rtz(x - rtz(x)) (res_neg = -1).  x - rtz(x) is exact in
+// fp32, so high part + residual carries x to about 2^-20 relative.
+__device__ __forceinline__ uint32_t split_pair(float x0, float x1, float res_neg) {
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  const h2v hi = __builtin_bit_cast(h2v, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+  const float r0 = fmaf(float(hi[0]), res_neg, x0);
+  const float r1 = fmaf(float(hi[1]), res_neg, x1);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+}
+
 constexpr int kWaves = 4;  // waves per workgroup; each walks its own pages of the work item
 
-template <int HD, int VGS>
+// Key-page mix of a pool: only M3 rows, only M0 4-bit codes, or both.
+enum KeyMode { KEYS_M3 = 0, KEYS_M0 = 1, KEYS_MIXED = 2 };
+
+template <int HD, int VGS, int VBITS>
 struct MfmaCfg {
-  static constexpr int KG = HD / 32;       // key groups of 32 channels (= contraction steps of the score)
-  static constexpr int VG = HD / VGS;      // value groups
-  static constexpr int H = VGS / 16;       // mix column tiles per value group
-  static constexpr int LPW4 = 128 / VGS;   // lanes sharing one 4-bit code word
-  static constexpr int NACC = VG * H;      // = HD / 16 accumulator tiles
-  static constexpr int NVR = HD / 32;      // 16-byte value-code pieces per lane per chunk (8-bit pages)
-  static constexpr int NSW = (16 * (HD / 16) + 63) / 64;  // scale words per lane per chunk (<= 16 G words)
-  // per-wave LDS: chunk staging -- value codes [VG][32][W] (W up to VGS / 4),
-  // value scales / biases and key scales / biases transposed to
-  // [group][32 tokens] fp16 -- later reused for the end-of-item rows
-  static constexpr int VPAY = VG * 32 * (VGS / 4);
+  static constexpr int KG = HD / 32;        // key groups of 32 channels (= contraction steps of the score)
+  static constexpr int VG = HD / VGS;       // value groups
+  static constexpr int H = VGS / 16;        // mix column tiles per value group
+  static constexpr int LPW4 = 128 / VGS;    // lanes sharing one 4-bit code word
+  static constexpr int NACC = VG * H;       // = HD / 16 accumulator tiles
+  static constexpr int W = VBITS == 8 ? VGS / 4 : VGS / 8;  // code words per (token, value group)
+  static constexpr int NVP = VG * 8 * W / 64;                // 16-byte value-code pieces per lane per chunk
+  static constexpr int NKS = (16 * KG + 63) / 64;            // key scale words per lane per chunk
+  static constexpr int NVS = (16 * VG + 63) / 64;            // value scale words per lane per chunk
+  // per-wave LDS: chunk staging -- value codes [VG][32][W], value scales /
+  // biases and key scales / biases transposed to [group][32 tokens] fp16 --
+  // later reused for the end-of-item rows
+  static constexpr int VPAY = VG * 32 * W;
   static constexpr int VSC = VPAY, VBS = VSC + 16 * VG, KSC = VBS + 16 * VG, KBS = KSC + 16 * KG;
   static constexpr int STAGE = KBS + 16 * KG;
   static constexpr int ROWS = 16 * HD + 16 * VG;  // D rows of the mix + bias sums
   static constexpr int WAVE_WORDS = STAGE > ROWS ? STAGE : ROWS;
   static constexpr int LDS_WORDS = kWaves * WAVE_WORDS;
+  static_assert(VG * 8 * W % 64 == 0, "value pieces must spread evenly over the wave");
 };
 
 // Registers one chunk needs from HBM.  The next chunk's loads are issued
-// into them as soon as the current chunk has consumed them (keys after its
-// score, values after staging), so they are in flight during its mix.
-template <int HD, int VGS>
+// into them as soon as the current chunk has consumed them (values and
+// scales after staging, keys after the score), so they are in flight during
+// its mix.  Every chunk issues the same loads whatever its page formats, so
+// the compiler never has to drain the queue to merge register versions.
+template <int HD, int VGS, int VBITS>
 struct ChunkRegs {
-  using Cfg = MfmaCfg<HD, VGS>;
-  u32x4 kr[2][Cfg::KG];     // key rows (M3: 8 fp16 per lane) or code words (M0: .x)
-  u32x4 vr[Cfg::NVR];       // value code pieces, blob byte order
-  uint32_t vs[Cfg::NSW], vb[Cfg::NSW], ks[Cfg::NSW], kbw[Cfg::NSW];  // scale / bias words
+  using Cfg = MfmaCfg<HD, VGS, VBITS>;
+  u32x4 kr[2][Cfg::KG];  // key rows (M3: 8 fp16) or the 16-byte code block of (token, group) (M0)
+  u32x4 vr[Cfg::NVP];    // value code pieces, blob byte order
+  uint32_t ks[Cfg::NKS], kbw[Cfg::NKS], vs[Cfg::NVS], vb[Cfg::NVS];  // scale / bias words
 };
 
 struct PageMeta {
   const uint8_t* kp;
   const uint8_t* vp;
-  int T;           // tokens to read (0: skip the page)
+  int T;  // tokens to read (0: skip the page)
   int kfmt, vfmt, vbits;
-  int64_t kscale_off, kbias_off, vscale_off, vbias_off;
+  uint32_t ksc, kbs, vsc, vbs;  // byte offsets of scales / biases in the blobs (0 where absent)
 };
 
-template <int HD, int VGS>
+template <int HD, int VGS, int KMODE, int VBITS, bool VM3>
 __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_kernel(DecodeArgs a) {
-  using Cfg = MfmaCfg<HD, VGS>;
-  using Regs = ChunkRegs<HD, VGS>;
-  constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4;
+  using Cfg = MfmaCfg<HD, VGS, VBITS>;
+  using Regs = ChunkRegs<HD, VGS, VBITS>;
+  constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W;
   __shared__ uint32_t lds_all[Cfg::LDS_WORDS];
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
   const dc_work_item it = a.items[blockIdx.x];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // readfirstlane tells the compiler the wave index is uniform, so page and
+  // chunk loop state, blob pointers and page metadata live in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r = lane & 15, kb = lane >> 4;
   const int nq = a.n_q;
   const int CAP = a.kpool.geometry.page_capacity;
@@ -136,27 +157,53 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
   uint16_t* kbs = reinterpret_cast<uint16_t*>(lds + Cfg::KBS);
 
   // ---- queries scaled by query_scale * log2(e); B fragments hi / residual ----
+  // lane (r, kb) holds channels 32 g + 8 kb + i of head r; one vector load per
+  // group.
   const int64_t qbase = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * nq * HD;
   const float qmul = a.q_scale * kLog2e;
+  const int64_t qrow = qbase + int64_t(r < nq ? r : 0) * HD + 8 * kb;
   Frag qhi[KG], qlo[KG];
   float qsum[KG];
-#pragma unroll
-  for (int g = 0; g < KG; ++g) {
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      v[i] = r < nq ? load_value(a.queries, a.queries_dtype, qbase + int64_t(r) * HD + 32 * g + 8 * kb + i) * qmul : 0.f;
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      qhi[g].u[i] = pack_h2(v[2 * i], v[2 * i + 1]);
-      qlo[g].u[i] = pack_h2(split_part(v[2 * i], true), split_part(v[2 * i + 1], true));
-      s += v[2 * i] + v[2 * i + 1];
+  auto setup_queries = [&]() {
+    float qv[KG][8];
+    if (a.queries_dtype == DC_F32) {
+      const float* q = reinterpret_cast<const float*>(a.queries) + qrow;
+  #pragma unroll
+      for (int g = 0; g < KG; ++g) {
+        const float4 x0 = *reinterpret_cast<const float4*>(q + 32 * g);
+        const float4 x1 = *reinterpret_cast<const float4*>(q + 32 * g + 4);
+        qv[g][0] = x0.x; qv[g][1] = x0.y; qv[g][2] = x0.z; qv[g][3] = x0.w;
+        qv[g][4] = x1.x; qv[g][5] = x1.y; qv[g][6] = x1.z; qv[g][7] = x1.w;
+      }
+    } else {
+      const uint16_t* q = reinterpret_cast<const uint16_t*>(a.queries) + qrow;
+      const bool bf = a.queries_dtype == DC_BF16;
+  #pragma unroll
+      for (int g = 0; g < KG; ++g) {
+        const uint4 x = *reinterpret_cast<const uint4*>(q + 32 * g);
+        const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[g][2 * i] = bf ? __uint_as_float(xs[i] << 16) : h2f(xs[i] & 0xffffu);
+          qv[g][2 * i + 1] = bf ? __uint_as_float(xs[i] & 0xffff0000u) : h2f(xs[i] >> 16);
+        }
+      }
     }
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
-    qsum[g] = s;  // sum over group g for head r
-  }
+  #pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      float s = 0.f;
+  #pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v0 = r < nq ? qv[g][2 * i] * qmul : 0.f, v1 = r < nq ? qv[g][2 * i + 1] * qmul : 0.f;
+        qhi[g].u[i] = pack_h2(v0, v1);
+        qlo[g].u[i] = pack_h2(split_part(v0, true), split_part(v1, true));
+        s += v0 + v1;
+      }
+      s += __shfl_xor(s, 16, 64);
+      s += __shfl_xor(s, 32, 64);
+      qsum[g] = s;  // sum over group g for head r
+    }
+  };
 
   // mix A-row role of this lane: high part (r < nq) or residual (nq <= r < 2 nq) of head qa
   const bool row_live = r < 2 * nq;
@@ -171,6 +218,18 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
   // mix column of this lane in tile h of value group g: d = VGS g + dcol + LPW4 h
   const int jj = r % LPW4, w4 = r / LPW4;
   const int dcol = 8 * w4 + jj;
+  const float res_neg = residual ? -1.f : 0.f;
+  // byte-permute selectors of this lane's code in tile h: the byte of token
+  // 2p into byte 0, of token 2p + 1 into byte 2 (4-bit: byte holding nibble
+  // jj + LPW4 h; 8-bit: byte (jj + LPW4 h) % 4)
+  uint32_t vsel[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    const uint32_t b = VBITS == 4 ? uint32_t((jj + LPW4 * h) >> 1) : uint32_t((jj + LPW4 * h) & 3);
+    vsel[h] = 0x0c000c00u | b | ((4u + b) << 16);
+  }
+  const uint32_t nib_mask = (jj & 1) ? 0x00f000f0u : 0x000f000fu;  // low or high nibble of the byte
+  const h2 nib_mul = (jj & 1) ? h2{(_Float16)0.0625f, (_Float16)0.0625f} : h2{(_Float16)1.f, (_Float16)1.f};
 
   f32x4 acc[Cfg::NACC];
 #pragma unroll
@@ -185,96 +244,84 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
   const int n_item = it.page_end - it.page_begin;
   const int np = n_item > wave ? (n_item - wave + kWaves - 1) / kWaves : 0;  // pages of this wave
 
-  // ---- loads of one chunk into registers: keys, then values ----
+  auto key_is_m3 = [&](const PageMeta& m) -> bool {
+    if constexpr (KMODE == KEYS_M3) return true;
+    if constexpr (KMODE == KEYS_M0) return false;
+    return m.kfmt == DC_FMT_M3_F16;
+  };
+  auto value_is_m0 = [&](const PageMeta& m) -> bool {
+    if constexpr (!VM3) return true;
+    return is_m0(m.vfmt);
+  };
+
+  // ---- loads of one chunk into registers (the same loads for every format) ----
   auto load_keys = [&](const PageMeta& m, int c0, Regs& R) {
-    if (m.kfmt == DC_FMT_M3_F16) {
-      const _Float16* K = reinterpret_cast<const _Float16*>(m.kp);
+    const bool km3 = key_is_m3(m);
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int ta = c0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+    for (int hh = 0; hh < 2; ++hh) {
+      const int ta = c0 + 8 * (r >> 2) + 4 * hh + (r & 3);
 #pragma unroll
-        for (int g = 0; g < KG; ++g) R.kr[hh][g] = *reinterpret_cast<const u32x4*>(K + ta * HD + 32 * g + 8 * kb);
+      for (int g = 0; g < KG; ++g) {
+        const int off = km3 ? (ta * HD + 32 * g + 8 * kb) * 2 : (g * CAP + ta) * 16;
+        R.kr[hh][g] = *reinterpret_cast<const u32x4*>(m.kp + off);
       }
-    } else {
-      const uint32_t* P = reinterpret_cast<const uint32_t*>(m.kp);
+    }
+    if constexpr (KMODE != KEYS_M3) {
+      const uint32_t* S = reinterpret_cast<const uint32_t*>(m.kp + m.ksc) + c0 * KG / 2;
+      const uint32_t* B = reinterpret_cast<const uint32_t*>(m.kp + m.kbs) + c0 * KG / 2;
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int ta = c0 + 8 * (r >> 2) + 4 * hh + (r & 3);
-#pragma unroll
-        for (int g = 0; g < KG; ++g) R.kr[hh][g].x = P[(g * CAP + ta) * 4 + kb];
-      }
-      const uint32_t* S = reinterpret_cast<const uint32_t*>(m.kp + m.kscale_off) + c0 * KG / 2;
-      const uint32_t* B = reinterpret_cast<const uint32_t*>(m.kp + m.kbias_off) + c0 * KG / 2;
-#pragma unroll
-      for (int k = 0; k < Cfg::NSW; ++k) {
-        const int e = lane + 64 * k;
-        if (e < 16 * KG) {
-          R.ks[k] = S[e];
-          if (m.kfmt == DC_FMT_M0_AFFINE) R.kbw[k] = B[e];
-        }
+      for (int k = 0; k < Cfg::NKS; ++k) {
+        const int e = (lane + 64 * k) % (16 * KG);
+        R.ks[k] = S[e];
+        R.kbw[k] = B[e];
       }
     }
   };
   auto load_values = [&](const PageMeta& m, int c0, Regs& R) {
-    if (is_m0(m.vfmt)) {
-      const int W = m.vbits == 8 ? VGS / 4 : VGS / 8;
-      const int per_g = 8 * W;
-      const u32x4* src = reinterpret_cast<const u32x4*>(m.vp);
 #pragma unroll
-      for (int k = 0; k < Cfg::NVR; ++k) {
-        const int e = lane + 64 * k;
-        if (e < VG * per_g) {
-          const int g = e / per_g, piece = e - g * per_g;
-          R.vr[k] = src[((g * CAP + c0) * W) / 4 + piece];
-        }
-      }
-      const uint32_t* S = reinterpret_cast<const uint32_t*>(m.vp + m.vscale_off) + c0 * VG / 2;
-      const uint32_t* B = reinterpret_cast<const uint32_t*>(m.vp + m.vbias_off) + c0 * VG / 2;
+    for (int k = 0; k < Cfg::NVP; ++k) {
+      const int e = lane + 64 * k;
+      const int g = e / (8 * W), piece = e - g * (8 * W);
+      R.vr[k] = *reinterpret_cast<const u32x4*>(m.vp + (((g * CAP + c0) * W) / 4 + piece) * 16);
+    }
+    const uint32_t* S = reinterpret_cast<const uint32_t*>(m.vp + m.vsc) + c0 * VG / 2;
+    const uint32_t* B = reinterpret_cast<const uint32_t*>(m.vp + m.vbs) + c0 * VG / 2;
 #pragma unroll
-      for (int k = 0; k < Cfg::NSW; ++k) {
-        const int e = lane + 64 * k;
-        if (e < 16 * VG) {
-          R.vs[k] = S[e];
-          if (m.vfmt == DC_FMT_M0_AFFINE) R.vb[k] = B[e];
-        }
-      }
+    for (int k = 0; k < Cfg::NVS; ++k) {
+      const int e = (lane + 64 * k) % (16 * VG);
+      R.vs[k] = S[e];
+      R.vb[k] = B[e];
     }
   };
 
   // ---- registers -> this wave's LDS staging area ----
-  auto stage_chunk = [&](const PageMeta& m, const Regs& R) {
-    if (is_m0(m.vfmt)) {
-      const int W = m.vbits == 8 ? VGS / 4 : VGS / 8;
-      u32x4* dst = reinterpret_cast<u32x4*>(lds);
+  auto stage_chunk = [&](const Regs& R) {
+    u32x4* dst = reinterpret_cast<u32x4*>(lds);
 #pragma unroll
-      for (int k = 0; k < Cfg::NVR; ++k) {
-        const int e = lane + 64 * k;
-        if (e < VG * 8 * W) dst[e] = R.vr[k];
-      }
-      // scale word e holds tokens / groups 2e and 2e + 1 of the [32][VG] array
+    for (int k = 0; k < Cfg::NVP; ++k) dst[lane + 64 * k] = R.vr[k];
+    // scale word e holds (token, group) entries 2e and 2e + 1 of the chunk's [32][G] array
 #pragma unroll
-      for (int k = 0; k < Cfg::NSW; ++k) {
-        const int e = lane + 64 * k;
-        if (e < 16 * VG) {
+    for (int k = 0; k < Cfg::NVS; ++k) {
+      const int e = lane + 64 * k;
+      if (e < 16 * VG) {
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const int hidx = 2 * e + s, t = hidx / VG, g = hidx - t * VG;
-            vsc[g * 32 + t] = uint16_t(R.vs[k] >> (16 * s));
-            if (m.vfmt == DC_FMT_M0_AFFINE) vbs[g * 32 + t] = uint16_t(R.vb[k] >> (16 * s));
-          }
+        for (int s = 0; s < 2; ++s) {
+          const int hidx = 2 * e + s, t = hidx / VG, g = hidx - t * VG;
+          vsc[g * 32 + t] = uint16_t(R.vs[k] >> (16 * s));
+          vbs[g * 32 + t] = uint16_t(R.vb[k] >> (16 * s));
         }
       }
     }
-    if (m.kfmt != DC_FMT_M3_F16) {
+    if constexpr (KMODE != KEYS_M3) {
 #pragma unroll
-      for (int k = 0; k < Cfg::NSW; ++k) {
+      for (int k = 0; k < Cfg::NKS; ++k) {
         const int e = lane + 64 * k;
         if (e < 16 * KG) {
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
             const int hidx = 2 * e + s, t = hidx / KG, g = hidx - t * KG;
             ksc[g * 32 + t] = uint16_t(R.ks[k] >> (16 * s));
-            if (m.kfmt == DC_FMT_M0_AFFINE) kbs[g * 32 + t] = uint16_t(R.kbw[k] >> (16 * s));
+            kbs[g * 32 + t] = uint16_t(R.kbw[k] >> (16 * s));
           }
         }
       }
@@ -283,9 +330,9 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
 
   // ---- score of one chunk: logits of this lane's chunk tokens 8 kb + e for head r ----
   auto score_chunk = [&](const PageMeta& m, const Regs& R, float* Ls) {
+    if (key_is_m3(m)) {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      if (m.kfmt == DC_FMT_M3_F16) {
+      for (int hh = 0; hh < 2; ++hh) {
         f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int g = 0; g < KG; ++g) {
@@ -296,16 +343,19 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = d[i];
-      } else {  // M0 4-bit, group 32: scale and bias applied per group in fp32
-        const bool k_affine = m.kfmt == DC_FMT_M0_AFFINE;
-        const float zp = k_affine ? 0.f : 7.f;
-        // (1024 + n_lo, 1024 + 16 n_hi) -> (n_lo - zp, n_hi - zp)
-        const h2 kmul = {(_Float16)1.f, (_Float16)0.0625f};
-        const h2 kadd = {(_Float16)(-1024.f - zp), (_Float16)(-64.f - zp)};
+      }
+    } else {  // M0 4-bit, group 32: scale and bias applied per group in fp32
+      const bool k_affine = m.kfmt == DC_FMT_M0_AFFINE;
+      const float zp = k_affine ? 0.f : 7.f;
+      // (1024 + n_lo, 1024 + 16 n_hi) -> (n_lo - zp, n_hi - zp)
+      const h2 kmul = {(_Float16)1.f, (_Float16)0.0625f};
+      const h2 kadd = {(_Float16)(-1024.f - zp), (_Float16)(-64.f - zp)};
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
         float Lh[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int g = 0; g < KG; ++g) {
-          const uint32_t w = R.kr[hh][g].x;
+          const uint32_t w = kb == 0 ? R.kr[hh][g].x : kb == 1 ? R.kr[hh][g].y : kb == 2 ? R.kr[hh][g].z : R.kr[hh][g].w;
           Frag ka;
 #pragma unroll
           for (int p = 0; p < 4; ++p) {
@@ -319,11 +369,11 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
           d = mfma(ka, qlo[g], d);
           // D rows 4 kb + i are chunk tokens 8 kb + 4 hh + i
           const uint2 sw = *reinterpret_cast<const uint2*>(ksc + g * 32 + 8 * kb + 4 * hh);
-          const uint2 bw = k_affine ? *reinterpret_cast<const uint2*>(kbs + g * 32 + 8 * kb + 4 * hh) : uint2{0u, 0u};
+          const uint2 bw = *reinterpret_cast<const uint2*>(kbs + g * 32 + 8 * kb + 4 * hh);
           const uint32_t sv[4] = {sw.x & 0xffffu, sw.x >> 16, sw.y & 0xffffu, sw.y >> 16};
           const uint32_t bv[4] = {bw.x & 0xffffu, bw.x >> 16, bw.y & 0xffffu, bw.y >> 16};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) Lh[i] += h2f(sv[i]) * d[i] + h2f(bv[i]) * qsum[g];
+          for (int i = 0; i < 4; ++i) Lh[i] += h2f(sv[i]) * d[i] + (k_affine ? h2f(bv[i]) * qsum[g] : 0.f);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = Lh[i];
@@ -364,20 +414,20 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
       for (int g = 0; g < VG; ++g) bsum[g] *= alpha;
     }
 
-    // mix: weights of this lane's A-row head on its 8 tokens
+    // weights of this lane's A-row head on its 8 tokens
     float pa[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float v = __shfl(Ls[e], pa_src, 64);
       pa[e] = row_live ? v : 0.f;
     }
-    if (is_m0(m.vfmt)) {
+    if (value_is_m0(m)) {
       const bool v_affine = m.vfmt == DC_FMT_M0_AFFINE;
-      const int vbits = m.vbits;
-      const int W = vbits == 8 ? VGS / 4 : VGS / 8;
-      const float zp = v_affine ? 0.f : float((1 << (vbits - 1)) - 1);
-      const uint32_t negb = h2_const(-1024.f - zp);
-      const uint32_t nib_shift = 4u * uint32_t(jj & 1);
+      const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
+      // codes become fp16 (1024 + c), or (1024 + 16 c) for a code in the high
+      // nibble of its byte; one packed fma maps either to c - zp exactly
+      const h2 vadd = VBITS == 4 && (jj & 1) ? h2{(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)}
+                                              : h2{(_Float16)(-1024.f - zp), (_Float16)(-1024.f - zp)};
 #pragma unroll
       for (int g = 0; g < VG; ++g) {
         const uint4 s8 = *reinterpret_cast<const uint4*>(vsc + g * 32 + 8 * kb);
@@ -385,51 +435,47 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
         Frag fa;
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const float x0 = pa[2 * pp] * h2f(sx[pp] & 0xffffu);
-          const float x1 = pa[2 * pp + 1] * h2f(sx[pp] >> 16);
-          fa.u[pp] = pack_h2(split_part(x0, residual), split_part(x1, residual));
+          const h2 sv = __builtin_bit_cast(h2, sx[pp]);
+          fa.u[pp] = split_pair(pa[2 * pp] * float(sv[0]), pa[2 * pp + 1] * float(sv[1]), res_neg);
         }
         if (v_affine) {
           const uint4 b8 = *reinterpret_cast<const uint4*>(vbs + g * 32 + 8 * kb);
           const uint32_t bx[4] = {b8.x, b8.y, b8.z, b8.w};
 #pragma unroll
-          for (int pp = 0; pp < 4; ++pp)
-            bsum[g] += Ls[2 * pp] * h2f(bx[pp] & 0xffffu) + Ls[2 * pp + 1] * h2f(bx[pp] >> 16);
+          for (int pp = 0; pp < 4; ++pp) {
+            const h2 bv = __builtin_bit_cast(h2, bx[pp]);
+            bsum[g] += Ls[2 * pp] * float(bv[0]) + Ls[2 * pp + 1] * float(bv[1]);
+          }
         }
         const uint32_t* Pw = lds + (g * 32 + 8 * kb) * W;  // words of tokens 8 kb + e
 #pragma unroll
         for (int h = 0; h < H; ++h) {
           Frag fb;
-          if (vbits == 4) {
-            const int nib = jj + LPW4 * h;  // low nibble of byte nib / 2 after the shift
-            const uint32_t sel = 0x0c000c00u | uint32_t(nib >> 1) | (uint32_t(4 + (nib >> 1)) << 16);
+          if constexpr (VBITS == 4) {
 #pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t w0 = Pw[(2 * pp) * W + w4] >> nib_shift;
-              const uint32_t w1 = Pw[(2 * pp + 1) * W + w4] >> nib_shift;
-              fb.u[pp] = magic_sub((__builtin_amdgcn_perm(w1, w0, sel) & 0x000f000fu) | 0x64006400u, negb);
+              const uint32_t x = __builtin_amdgcn_perm(Pw[(2 * pp + 1) * W + w4], Pw[(2 * pp) * W + w4], vsel[h]);
+              const h2 c = __builtin_bit_cast(h2, (x & nib_mask) | 0x64006400u) * nib_mul + vadd;
+              fb.u[pp] = __builtin_bit_cast(uint32_t, c);
             }
           } else {
-            const int e8 = jj + LPW4 * h;  // channel dcol + LPW4 h = word 2 w4 + e8 / 4, byte e8 % 4
-            const int wsel = 2 * w4 + (e8 >> 2);
-            const uint32_t sel = 0x0c000c00u | uint32_t(e8 & 3) | (uint32_t(4 + (e8 & 3)) << 16);
+            const int wsel = 2 * w4 + ((jj + LPW4 * h) >> 2);  // channel dcol + LPW4 h: word 2 w4 + e / 4, byte e % 4
 #pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t w0 = Pw[(2 * pp) * W + wsel];
-              const uint32_t w1 = Pw[(2 * pp + 1) * W + wsel];
-              fb.u[pp] = magic_sub(__builtin_amdgcn_perm(w1, w0, sel) | 0x64006400u, negb);
+              const uint32_t x = __builtin_amdgcn_perm(Pw[(2 * pp + 1) * W + wsel], Pw[(2 * pp) * W + wsel], vsel[h]);
+              const h2 c = __builtin_bit_cast(h2, x | 0x64006400u) + vadd;
+              fb.u[pp] = __builtin_bit_cast(uint32_t, c);
             }
           }
           acc[g * H + h] = mfma(fa, fb, acc[g * H + h]);
         }
-        // keep the scheduler from hoisting every group's LDS reads at once
-        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_barrier(0);  // keep every group's LDS reads from being hoisted at once
       }
-    } else {  // M3 fp16 values (the exact recent window): gather columns from the rows
+    } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): gather columns from the rows
       const uint16_t* V = reinterpret_cast<const uint16_t*>(m.vp);
       Frag fa;
 #pragma unroll
-      for (int pp = 0; pp < 4; ++pp) fa.u[pp] = pack_h2(split_part(pa[2 * pp], residual), split_part(pa[2 * pp + 1], residual));
+      for (int pp = 0; pp < 4; ++pp) fa.u[pp] = split_pair(pa[2 * pp], pa[2 * pp + 1], res_neg);
 #pragma unroll
       for (int g = 0; g < VG; ++g)
 #pragma unroll
@@ -449,11 +495,14 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
   };
 
   // ---- walk this wave's pages: page meta 64 pages at a time, chunks pipelined ----
-  for (int base = 0; base < np; base += 64) {
+  // lane i < nb holds the ids / descriptors of the wave's page base + i; the
+  // first batch is fetched before the query setup so the two overlap
+  uint32_t k0 = 0, k1 = 0, v0 = 0, v1 = 0;
+  int ok = 0;
+  auto load_meta = [&](int base) {
     const int nb = np - base < 64 ? np - base : 64;
-    // lane i < nb holds the ids / descriptors of the wave's page base + i
-    uint32_t k0 = 0, k1 = 0, v0 = 0, v1 = 0;
-    int ok = 0;
+    k0 = k1 = v0 = v1 = 0u;
+    ok = 0;
     if (lane < nb) {
       const int p = it.page_begin + wave + kWaves * (base + lane);
       const int kid = a.k_table[trow + p], vid = a.v_table[trow + p];
@@ -464,6 +513,12 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
         ok = 1;
       }
     }
+  };
+  if (np > 0) load_meta(0);
+  setup_queries();
+  for (int base = 0; base < np; base += 64) {
+    const int nb = np - base < 64 ? np - base : 64;
+    if (base > 0) load_meta(base);
     auto meta_of = [&](int i) -> PageMeta {
       PageMeta m{};
       const uint32_t kw0 = __builtin_amdgcn_readlane(k0, i), kw1 = __builtin_amdgcn_readlane(k1, i);
@@ -484,44 +539,56 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
       m.kfmt = kd.format;
       m.vfmt = vd.format;
       m.vbits = vd.bits;
-      m.kscale_off = KL.scales_off;
-      m.kbias_off = KL.bias_off;
-      m.vscale_off = VL.scales_off;
-      m.vbias_off = VL.bias_off;
+      const bool km0 = is_m0(kd.format), vm0 = is_m0(vd.format);
+      m.ksc = km0 ? uint32_t(KL.scales_off) : 0u;
+      m.kbs = kd.format == DC_FMT_M0_AFFINE ? uint32_t(KL.bias_off) : m.ksc;
+      m.vsc = vm0 ? uint32_t(VL.scales_off) : 0u;
+      m.vbs = vd.format == DC_FMT_M0_AFFINE ? uint32_t(VL.bias_off) : m.vsc;
       return m;
     };
 
     int i = 0;
     PageMeta cur = meta_of(0);
-    while (i < nb && cur.T <= 0) {
-      ++i;
-      if (i < nb) cur = meta_of(i);
-    }
-    if (i >= nb) continue;
+    while (cur.T <= 0 && i + 1 < nb) cur = meta_of(++i);
+    if (cur.T <= 0) continue;
     int c0 = 0;
     Regs R;
     load_keys(cur, c0, R);
     load_values(cur, c0, R);
     while (true) {
-      // next chunk of this batch, if any
+      // next chunk of this batch; the current chunk again when there is none
       int ni = i, nc0 = c0 + 32;
       PageMeta nm = cur;
       if (nc0 >= cur.T) {
         nc0 = 0;
-        do {
+        ni = i + 1;
+        while (ni < nb) {
+          nm = meta_of(ni);
+          if (nm.T > 0) break;
           ++ni;
-          if (ni < nb) nm = meta_of(ni);
-        } while (ni < nb && nm.T <= 0);
+        }
       }
       const bool more = ni < nb;
-      stage_chunk(cur, R);  // value codes and scales -> LDS; frees their registers
+      if (!more) {
+        nm = cur;
+        nc0 = c0;
+      }
       float Ls[8];
-      score_chunk(cur, R, Ls);  // frees the key registers
-      if (more) {  // the next chunk's loads fly while this one is mixed
+      if constexpr (HD <= 128) {
+        Regs Rn;  // the next chunk's loads fly while this one is scored and mixed
+        load_keys(nm, nc0, Rn);
+        load_values(nm, nc0, Rn);
+        stage_chunk(R);  // value codes and scales -> LDS
+        score_chunk(cur, R, Ls);
+        mix_chunk(cur, c0, Ls);
+        R = Rn;
+      } else {  // one register set: reload it as soon as the chunk has consumed it
+        stage_chunk(R);
+        score_chunk(cur, R, Ls);
         load_keys(nm, nc0, R);
         load_values(nm, nc0, R);
+        mix_chunk(cur, c0, Ls);
       }
-      mix_chunk(cur, c0, Ls);
       if (!more) break;
       cur = nm;
       i = ni;
@@ -596,39 +663,59 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
   }
 }
 
-template <int HD, int VGS>
+template <int HD, int VGS, int KMODE, int VBITS, bool VM3>
 static int launch_t(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS>), dim3(uint32_t(a.n_items)), dim3(kWaves * 64), 0, stream, a);
+  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, VBITS, VM3>), dim3(uint32_t(a.n_items)), dim3(kWaves * 64),
+                     0, stream, a);
   return check_hip(hipGetLastError(), "decode_mfma_kernel launch");
 }
 
-// Formats the fast path reads (bit = format * 9 + bits, as in dc_pool).
 static constexpr uint64_t fbit(int fmt, int bits) { return uint64_t(1) << (fmt * 9 + bits); }
-
-static bool fast_formats(uint64_t kmask, uint64_t vmask) {
-  const uint64_t k_ok = fbit(DC_FMT_M3_F16, 0) | fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
-  const uint64_t v_ok = k_ok | fbit(DC_FMT_M0_AFFINE, 8) | fbit(DC_FMT_M0_SYMMETRIC, 8);
-  return kmask != 0 && vmask != 0 && (kmask & ~k_ok) == 0 && (vmask & ~v_ok) == 0;
-}
 
 int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) {
   *launched = false;
   const dc_page_geometry& kg = a.kpool.geometry;
   const dc_page_geometry& vg = a.vpool.geometry;
   if (a.n_q > 8 || kg.layout != 0 || vg.layout != 0 || kg.group_size != 32) return DC_OK;
-  if (!fast_formats(a.kpool.format_mask, a.vpool.format_mask)) return DC_OK;
-  const int hd = kg.head_dim, vgs = vg.group_size;
   if (kg.page_capacity % 32 != 0) return DC_OK;
+  // formats present in the pools (bit = format * 9 + bits, as in dc_pool)
+  const uint64_t km = a.kpool.format_mask, vm = a.vpool.format_mask;
+  const uint64_t k_m3 = fbit(DC_FMT_M3_F16, 0), k_m0 = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
+  const uint64_t v4 = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
+  const uint64_t v8 = fbit(DC_FMT_M0_AFFINE, 8) | fbit(DC_FMT_M0_SYMMETRIC, 8);
+  if (km == 0 || vm == 0 || (km & ~(k_m3 | k_m0)) || (vm & ~(k_m3 | v4 | v8))) return DC_OK;
+  if ((vm & v4) && (vm & v8)) return DC_OK;  // one value code width per launch
+  const int kmode = (km & k_m3) && (km & k_m0) ? KEYS_MIXED : (km & k_m3) ? KEYS_M3 : KEYS_M0;
+  const int vbits = (vm & v8) ? 8 : 4;
+  const bool vm3 = (vm & k_m3) != 0;
+  const int hd = kg.head_dim, vgs = vg.group_size;
   int rc = -1;
-#define DC_TRY(HD_, VGS_) \
-  if (hd == HD_ && vgs == VGS_) rc = launch_t<HD_, VGS_>(a, stream);
-  DC_TRY(64, 32)
-  DC_TRY(64, 64)
-  DC_TRY(128, 32)
-  DC_TRY(128, 64)
-  DC_TRY(256, 32)
-  DC_TRY(256, 64)
-#undef DC_TRY
+  // specialised instantiations for common pools, a general one per shape otherwise
+#define DC_EXACT(HD_, VGS_, KM_, VB_, VM3_)                                                          \
+  if (rc < 0 && hd == HD_ && vgs == VGS_ && kmode == KM_ && vbits == VB_ && vm3 == VM3_) \
+    rc = launch_t<HD_, VGS_, KM_, VB_, VM3_>(a, stream);
+#define DC_GENERAL(HD_, VGS_, VB_) \
+  if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_) rc = launch_t<HD_, VGS_, KEYS_MIXED, VB_, true>(a, stream);
+  DC_EXACT(64, 32, KEYS_M0, 4, false)
+  DC_EXACT(128, 32, KEYS_M3, 4, false)
+  DC_EXACT(128, 32, KEYS_M0, 4, false)
+  DC_EXACT(128, 64, KEYS_MIXED, 8, false)
+  DC_EXACT(128, 64, KEYS_M0, 8, false)
+  DC_EXACT(256, 32, KEYS_M0, 4, false)
+  DC_GENERAL(64, 32, 4)
+  DC_GENERAL(64, 32, 8)
+  DC_GENERAL(64, 64, 4)
+  DC_GENERAL(64, 64, 8)
+  DC_GENERAL(128, 32, 4)
+  DC_GENERAL(128, 32, 8)
+  DC_GENERAL(128, 64, 4)
+  DC_GENERAL(128, 64, 8)
+  DC_GENERAL(256, 32, 4)
+  DC_GENERAL(256, 32, 8)
+  DC_GENERAL(256, 64, 4)
+  DC_GENERAL(256, 64, 8)
+#undef DC_EXACT
+#undef DC_GENERAL
   if (rc < 0) return DC_OK;
   *launched = true;
   return rc;

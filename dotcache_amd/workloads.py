@@ -189,9 +189,11 @@ def _gen(shape, gen, dist: str, device):
 
 
 def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | None = None, batch: int | None = None,
-                   context: int | None = None, pages_per_split: int | None = None) -> Workload:
+                   context: int | None = None, pages_per_split: int | None = None,
+                   scatter_pages: bool = True) -> Workload:
     """Encode every layer's pages on the device and build its page tables.
-    ``layers`` / ``batch`` / ``context`` shrink the workload for tests."""
+    ``layers`` / ``batch`` / ``context`` shrink the workload for tests;
+    ``scatter_pages=False`` keeps each sequence's pages in allocation order."""
     torch = _torch()
     spec = SPECS[name]
     if layers is not None or batch is not None or context is not None:
@@ -237,7 +239,7 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
             kid = k_pool.allocate(*kfmt.fmt, nph)
             vid = v_pool.allocate(*spec.value.fmt, nph)
             # scatter each (sequence, head)'s pages across the pool
-            perm = rng.permutation(nph)
+            perm = rng.permutation(nph) if scatter_pages else np.arange(nph)
             kid, vid = kid[perm], vid[perm]
             off = 0
             for b in range(B):
