@@ -42,7 +42,21 @@ def parse():
                     help="keep each sequence's pages in allocation order instead of scattering them over the pool")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only copy a BYTES-sized device buffer three times and exit: the known-size "
+                         "transfer that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
+
+
+def copy_probe(nbytes: int) -> None:
+    import torch
+
+    src = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {nbytes} bytes x3")
 
 
 def cpu_baseline(wl, budget_s: float) -> dict:
@@ -53,7 +67,6 @@ def cpu_baseline(wl, budget_s: float) -> dict:
     tokens x (query heads done / query heads) / seconds."""
     from threadpoolctl import threadpool_limits
 
-    from dotcache_amd.types import PageHeader
     from oracle import dotcache_oracle as O
 
     spec = wl.spec
@@ -63,20 +76,8 @@ def cpu_baseline(wl, budget_s: float) -> dict:
     vt = lt.v_table[0].cpu().numpy()
     q_all = wl.queries[0][0].float().cpu().numpy() * wl.query_scale  # [H, Q, hd]
 
-    def hdr(kind, geo, fmt, bits, T):
-        from dotcache_amd import _lib
-        mode = "M3" if fmt == _lib.FMT_M3_F16 else "M0"
-        scheme = "symmetric" if fmt == _lib.FMT_M0_SYMMETRIC else "affine"
-        G = -(-geo.head_dim // geo.group_size)
-        b = bits if mode == "M0" else 4
-        return PageHeader(layer_id=0, kv_head_id=0, kind=kind, token_start=0, token_count=T, head_dim=geo.head_dim,
-                          padded_head_dim=G * geo.group_size, group_size=geo.group_size, num_groups=G, bits=b,
-                          words_per_group=(geo.group_size * b + 31) // 32, mode_default=mode, layout="group_major",
-                          quant_scheme=scheme)
-
     def to_oracle(pool, pid, kind):
-        d = pool.desc(pid)
-        page = pool.download_page(int(pid), hdr(kind, pool.geometry, int(d["format"]), int(d["bits"]), int(d["tokens"])))
+        page = pool.download_page(int(pid), kind=kind)
         oh = O.OracleHeader(**page.header.to_dict())
         return O.OraclePage(header=oh, payload=page.payload, scales=page.scales, bias=page.bias,
                             escape_payload=page.escape_payload, escape_scales=page.escape_scales)
@@ -114,6 +115,10 @@ def main():
               "The path shards by (sequence, KV head) with no exchange, see DESIGN.md.", file=sys.stderr)
         sys.exit(2)
     import torch
+
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     from dotcache_amd.workloads import SPECS, build_workload
 

@@ -193,26 +193,64 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
   }
 }
 
-// One block per merge item, one thread per channel: combine partials s with
-// weights exp2(m_s - M) (log2 domain), then divide by the merged sum.
+// One block per merge item.  Wave j < n_q reduces the partials' (m, l) of
+// query head j to (M, L) in LDS; then every thread combines four channels:
+// out = sum_s o_s exp2(m_s - M) / L (log2 domain).
 __global__ void __launch_bounds__(256) merge_kernel(const dc_merge_item* __restrict__ merges, const float* part_o,
                                                     const float* part_ml, float* out, int32_t n_kv_heads,
                                                     int32_t nq, int32_t hd, int64_t max_partials) {
+  __shared__ float sM[kMaxQ], sL[kMaxQ];
   const dc_merge_item mi = merges[blockIdx.x];
-  const int32_t j = blockIdx.y;
-  if (mi.partial_begin < 0 || mi.count <= 0 || mi.partial_begin + mi.count > max_partials) return;
-  for (int32_t c = threadIdx.x; c < hd; c += blockDim.x) {
+  if (mi.partial_begin < 0 || mi.count <= 0 || int64_t(mi.partial_begin) + mi.count > max_partials) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float* ml = part_ml + int64_t(mi.partial_begin) * nq * 2;
+  for (int j = wave; j < nq; j += blockDim.x >> 6) {
     float M = -INFINITY;
-    for (int32_t s = 0; s < mi.count; ++s) M = fmaxf(M, part_ml[(int64_t(mi.partial_begin + s) * nq + j) * 2]);
-    float L = 0.f, O = 0.f;
-    for (int32_t s = 0; s < mi.count; ++s) {
-      const int64_t ps = mi.partial_begin + s;
-      const float m = part_ml[(ps * nq + j) * 2], l = part_ml[(ps * nq + j) * 2 + 1];
-      const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-      L += l * w;
-      O += part_o[(ps * nq + j) * hd + c] * w;
+    for (int s = lane; s < mi.count; s += 64) M = fmaxf(M, ml[(int64_t(s) * nq + j) * 2]);
+    M = wave_max(M);
+    float L = 0.f;
+    for (int s = lane; s < mi.count; s += 64) {
+      const float m = ml[(int64_t(s) * nq + j) * 2];
+      L += m == -INFINITY ? 0.f : ml[(int64_t(s) * nq + j) * 2 + 1] * exp2f(m - M);
     }
-    out[((int64_t(mi.seq) * n_kv_heads + mi.kv_head) * nq + j) * hd + c] = O / fmaxf(L, 1e-30f);
+    L = wave_sum(L);
+    if (lane == 0) {
+      sM[j] = M;
+      sL[j] = L;
+    }
+  }
+  __syncthreads();
+  const float* po = part_o + int64_t(mi.partial_begin) * nq * hd;
+  float* o = out + (int64_t(mi.seq) * n_kv_heads + mi.kv_head) * nq * hd;
+  if ((hd & 3) == 0 && ((reinterpret_cast<uintptr_t>(po) | reinterpret_cast<uintptr_t>(o)) & 15) == 0) {
+    // four channels of one head per thread, 16-byte accesses
+    for (int idx = 4 * threadIdx.x; idx < nq * hd; idx += 4 * blockDim.x) {
+      const int j = idx / hd;
+      const float M = sM[j];
+      float4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < mi.count; ++s) {
+        const float m = ml[(int64_t(s) * nq + j) * 2];
+        const float w = m == -INFINITY ? 0.f : exp2f(m - M);
+        const float4 v = *reinterpret_cast<const float4*>(po + int64_t(s) * nq * hd + idx);
+        acc.x += v.x * w;
+        acc.y += v.y * w;
+        acc.z += v.z * w;
+        acc.w += v.w * w;
+      }
+      const float inv = 1.f / fmaxf(sL[j], 1e-30f);
+      *reinterpret_cast<float4*>(o + idx) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < nq * hd; idx += blockDim.x) {
+      const int j = idx / hd;
+      const float M = sM[j];
+      float acc = 0.f;
+      for (int s = 0; s < mi.count; ++s) {
+        const float m = ml[(int64_t(s) * nq + j) * 2];
+        acc += m == -INFINITY ? 0.f : po[int64_t(s) * nq * hd + idx] * exp2f(m - M);
+      }
+      o[idx] = acc / fmaxf(sL[j], 1e-30f);
+    }
   }
 }
 
@@ -232,7 +270,7 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
 
 int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream) {
   if (n_merges <= 0) return DC_OK;
-  hipLaunchKernelGGL(merge_kernel, dim3(uint32_t(n_merges), uint32_t(a.n_q)), dim3(256), 0, stream, merges,
+  hipLaunchKernelGGL(merge_kernel, dim3(uint32_t(n_merges)), dim3(256), 0, stream, merges,
                      a.part_o, a.part_ml, a.out, a.n_kv_heads, a.n_q, a.kpool.geometry.head_dim, a.max_partials);
   return check_hip(hipGetLastError(), "merge_kernel launch");
 }

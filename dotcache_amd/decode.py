@@ -20,11 +20,11 @@ import numpy as np
 from . import _lib
 from .page_pool import DevicePagePool, current_stream_ptr, dtype_code
 
-# Split long page lists so a launch has about two workgroups (of four
-# wavefronts) per CU for the 256 CUs, but keep each item long enough that every
-# wavefront walks a few pages and the split-K partials stay a small fraction
-# of the bytes read.
-DEFAULT_TARGET_ITEMS = 512
+# Split long page lists so a launch has about one workgroup (of four
+# wavefronts) per CU for the 256 CUs: every wavefront then walks several pages,
+# which amortises its fixed cost (query set-up, the first loads, the final
+# combine) and keeps the split-K partials a small fraction of the bytes read.
+DEFAULT_TARGET_ITEMS = 256
 MIN_PAGES_PER_SPLIT = 4
 
 

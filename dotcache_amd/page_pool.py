@@ -299,17 +299,32 @@ class DevicePagePool:
         self._dirty = True
         return ids
 
-    def download_page(self, page_id: int, header: PageHeader | None = None) -> EncodedPage:
-        """Read one page back into a host :class:`EncodedPage` (reference layout)."""
+    def header_of(self, page_id: int, kind: str = "K") -> PageHeader:
+        """A reference page header for a page written on the device (by
+        ``encode_rows``), from its descriptor and the pool geometry."""
+        d = self._host_desc[int(page_id)]
+        fmt, bits = int(d["format"]), int(d["bits"])
+        g = self.geometry
+        m0 = fmt in (_lib.FMT_M0_AFFINE, _lib.FMT_M0_SYMMETRIC)
+        b = bits if m0 else 4
+        esc = {_lib.FMT_M3_F32: "float32", _lib.FMT_M3_I8: "int8"}.get(fmt, "float16")
+        return PageHeader(layer_id=0, kv_head_id=0, kind=kind, token_start=0, token_count=int(d["tokens"]),
+                          head_dim=g.head_dim, padded_head_dim=g.num_groups * g.group_size, group_size=g.group_size,
+                          num_groups=g.num_groups, bits=b, words_per_group=words_per_group(g.group_size, b),
+                          mode_default="M0" if m0 else "M3", layout=g.layout,
+                          quant_scheme="symmetric" if fmt == _lib.FMT_M0_SYMMETRIC else "affine", escape_dtype=esc)
+
+    def download_page(self, page_id: int, header: PageHeader | None = None, *, kind: str = "K") -> EncodedPage:
+        """Read one page back into a host :class:`EncodedPage` (reference
+        layout).  The header is ``header``, the one stored at upload, or one
+        made from the descriptor (``kind`` names K or V pages)."""
         d = self._host_desc[int(page_id)]
         fmt, bits, T = int(d["format"]), int(d["bits"]), int(d["tokens"])
         g = self.geometry
         cap = g.page_capacity
         start = int(d["block"]) * 256
         blob = self.arena[start: start + self.blob_bytes(fmt, bits)].cpu().numpy()
-        h = header or self.headers.get(int(page_id))
-        if h is None:
-            raise ValueError("page has no header; pass one")
+        h = header or self.headers.get(int(page_id)) or self.header_of(page_id, kind)
         h = PageHeader.from_dict(h.to_dict())
         h.token_count = T
         if fmt in (_lib.FMT_M0_AFFINE, _lib.FMT_M0_SYMMETRIC):

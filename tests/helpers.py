@@ -25,3 +25,27 @@ def hard_values(rng, t, hd, *, outliers=True):
     if t > 3:
         x[3, 0] = -0.0
     return x
+
+
+def pool_page_to_oracle(pool, page_id, kind):
+    """Download one device page (written by the product) as an oracle page."""
+    from oracle import dotcache_oracle as O
+
+    page = pool.download_page(int(page_id), kind=kind)
+    return O.OraclePage(header=O.OracleHeader(**page.header.to_dict()), payload=page.payload, scales=page.scales,
+                        bias=page.bias, escape_payload=page.escape_payload, escape_scales=page.escape_scales)
+
+
+def workload_oracle(wl, layer, b, h):
+    """Oracle decode of (layer, sequence b, KV head h) of a built workload:
+    ``[n_q, head_dim]`` from the pages as they sit in the pools now."""
+    from oracle import dotcache_oracle as O
+
+    lt = wl.layers[layer]
+    n = int(lt.seq_pages[b])
+    kt = lt.k_table[b, h, :n].cpu().numpy()
+    vt = lt.v_table[b, h, :n].cpu().numpy()
+    kp = [pool_page_to_oracle(wl.k_pool, p, "K") for p in kt]
+    vp = [pool_page_to_oracle(wl.v_pool, p, "V") for p in vt]
+    q = wl.queries[layer][b, h].float().cpu().numpy() * wl.query_scale
+    return O.decode_multi_query_step(q, kp, vp)[2]

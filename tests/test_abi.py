@@ -82,6 +82,10 @@ def test_planner_rejects_empty_sequence():
         _plan([3, 0], 1, 2)
 
 
+def test_workspace_holds_the_partials():
+    assert _lib.lib().dc_decode_workspace_bytes(10, 7, 128) == 10 * 7 * 130 * 4
+
+
 def test_planner_reports_short_tables():
     sp = np.asarray([100], dtype=np.int32)
     ni, nm, npart = C.c_int32(), C.c_int32(), C.c_int32()

@@ -1,0 +1,74 @@
+"""The benchmark workloads end to end: pages encoded on the device into the
+pools, one fused ``dc_decode_paged`` launch per layer (plus the per-step
+append for config 5), checked against the oracle run on the same pages
+downloaded from the device.  Reduced sizes cover every configuration; the
+full config 3 shape is checked on sampled (sequence, KV head) streams."""
+import numpy as np
+import pytest
+
+from tests.helpers import workload_oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # max-abs error bound on the attention output
+
+
+def _check(wl, layer, pairs):
+    out = wl.outs[layer].cpu().numpy()
+    for b, h in pairs:
+        want = workload_oracle(wl, layer, b, h)
+        err = float(np.max(np.abs(out[b, h] - want)))
+        assert err < TOL, f"{wl.spec.name} layer {layer} seq {b} head {h}: max-abs error {err}"
+
+
+@pytest.mark.parametrize("name,context", [("c1", None), ("c2", 700), ("c3", 1500), ("c4", None), ("c5", 1000)])
+def test_workload_step_matches_oracle(name, context):
+    import torch
+
+    from dotcache_amd.workloads import build_workload
+
+    print(f"workload {name} context {context}", flush=True)
+    batch = {"c1": None, "c4": 2}.get(name, 3)
+    wl = build_workload(name, seed=3, layers=2, batch=batch, context=context, pages_per_split=2)
+    for _ in range(2):  # twice: a step must leave the pools and workspace ready for the next
+        wl.step()
+    torch.cuda.synchronize()
+    B, H = wl.spec.batch, wl.spec.n_kv_heads
+    for layer in range(2):
+        _check(wl, layer, [(b, h) for b in range(B) for h in range(H)])
+
+
+def test_workspace_reused_across_plans():
+    """One workspace serves plans with different split counts in turn."""
+    import torch
+
+    from dotcache_amd.decode import decode_paged, make_plan
+    from dotcache_amd.workloads import build_workload
+
+    wl = build_workload("c3", seed=4, layers=1, batch=3, context=1300)
+    lt = wl.layers[0]
+    H = wl.spec.n_kv_heads
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    outs = []
+    for pps in (2, None, 3, 1, 2):
+        plan = make_plan(lt.seq_pages, H, pps)
+        out = decode_paged(wl.k_pool, lt.k_table, lt.v_table, lt.seq_pages, wl.queries[0],
+                           query_scale=wl.query_scale, plan=plan, workspace=ws, validate=True, v_pool=wl.v_pool)
+        outs.append(out.cpu().numpy())
+    for o in outs[1:]:
+        assert np.max(np.abs(o - outs[0])) < 2e-5
+    wl.outs[0].copy_(torch.from_numpy(outs[0]))
+    _check(wl, 0, [(b, h) for b in range(3) for h in range(H)])
+
+
+def test_full_size_c3_sampled_streams():
+    """Config 3 at its full shape (batch 8 x 16384 tokens, hd 128, GQA 7,
+    one layer): streams of the first and last sequence against the oracle."""
+    import torch
+
+    from dotcache_amd.workloads import build_workload
+
+    wl = build_workload("c3", seed=0, layers=1)
+    wl.step()
+    torch.cuda.synchronize()
+    _check(wl, 0, [(0, 0), (0, 3), (7, 1), (7, 2)])
