@@ -40,6 +40,10 @@ def parse():
     ap.add_argument("--pages-per-split", type=int, default=None)
     ap.add_argument("--contiguous-pages", action="store_true",
                     help="keep each sequence's pages in allocation order instead of scattering them over the pool")
+    ap.add_argument("--decode-path", default="auto", choices=["auto", "generic"],
+                    help="auto: the MFMA kernel where the pages fit it; generic: the VALU kernel only")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel from Python each step instead of replaying captured HIP graphs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -120,43 +124,57 @@ def main():
         copy_probe(args.copy_probe)
         return
 
+    from dotcache_amd.decode import set_decode_path
     from dotcache_amd.workloads import SPECS, build_workload
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
     t0 = time.time()
     log(f"building workload {args.config} ...")
+    set_decode_path(args.decode_path)
     wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
                         scatter_pages=not args.contiguous_pages)
     spec = wl.spec
     log(f"built in {time.time() - t0:.1f} s: {wl.plan.n_items} work items/layer, pages/split {wl.plan.pages_per_split}, "
         f"K pool {wl.k_pool.arena.numel() / 1e9:.2f} GB, V pool {wl.v_pool.arena.numel() / 1e9:.2f} GB")
 
+    if not args.eager:
+        wl.capture()  # the whole step (every layer's kernels) as one HIP graph
     for _ in range(args.warmup):
         wl.step()
     torch.cuda.synchronize()
 
+    # All events are recorded on torch's current stream, the stream the
+    # library's kernels are launched on.  Nothing is recorded between the
+    # kernels of a step: an event between two kernels costs more than the
+    # gap it measures.
     L = spec.n_layers
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
-          for _ in range(args.steps)]
-    cur = {"s": 0}
 
-    def hook(l, what):
-        e = ev[cur["s"]][l][0 if what == "begin" else 1]
-        e.record()
+    def timed(fn, n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b)
 
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for s in range(args.steps):
-        cur["s"] = s
-        wl.step(layer_hook=hook)
-    end.record()
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    ms_step = total_ms / args.steps
-    layer_ms = np.array([[b.elapsed_time(e) for (b, e) in row] for row in ev])
-    launch_ms = float(layer_ms.mean())
+    # (1) the benchmark proper: exactly K whole steps
+    ms_step = timed(wl.step, args.steps) / args.steps
+
+    # (2) the dominant kernel alone: the K steps' decode launches back to
+    # back (partials left in the workspace), then (3) the merges alone
+    def decode_all():
+        for l in range(L):
+            wl.decode_kernel(l)
+
+    def merge_all():
+        for l in range(L):
+            wl.merge_kernel(l)
+
+    launch_ms = timed(decode_all, args.steps) / (args.steps * L)
+    merge_ms = timed(merge_all, args.steps) / (args.steps * L)
 
     bytes_step = wl.algorithmic_bytes_per_step()
     pos_step = wl.token_positions_per_step()
@@ -165,7 +183,8 @@ def main():
     bytes_launch = bytes_step / L
     achieved = bytes_launch / (launch_ms / 1e3) / 1e9
     log(f"{ms_step:.3f} ms/step, {value / 1e9:.3f} G tokens/s, {gbps:.0f} GB/s over the step; "
-        f"decode launch {launch_ms * 1e3:.1f} us -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak)")
+        f"decode kernel {launch_ms * 1e3:.1f} us -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak), "
+        f"merge {merge_ms * 1e3:.1f} us")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -200,6 +219,7 @@ def main():
             "value_pages": fmt(spec.value),
             "append": spec.append,
             "pages_per_split": wl.plan.pages_per_split,
+            "launch": "eager" if args.eager else "hip graph of the whole step",
             "parallelism": "single GPU",
         },
         "hbm_gbps": gbps,
@@ -213,9 +233,12 @@ def main():
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
             "traffic": None,
-            "kernel": "dc_decode_paged (per-layer launch)",
+            "kernel": ("decode_mfma_kernel" if args.decode_path == "auto" else "decode_generic_kernel")
+                      + " (dc_decode_paged, one launch per layer)",
             "launch_us": launch_ms * 1e3,
             "bytes_per_launch": bytes_launch,
+            "merge_us": merge_ms * 1e3,
+            "decode_path": args.decode_path,
         },
         "cpu_baseline": cpu,
     }

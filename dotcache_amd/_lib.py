@@ -70,6 +70,8 @@ SIGNATURES = {
                                   C.c_void_p, C.c_int64, C.c_void_p]),
     "dc_decode_workspace_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32]),
     "dc_set_decode_path": (C.c_int, [C.c_int32]),
+    "dc_lse_merge": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                               C.c_void_p, C.c_void_p]),
 }
 
 _lib: C.CDLL | None = None

@@ -193,63 +193,52 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
   }
 }
 
-// One block per merge item.  Wave j < n_q reduces the partials' (m, l) of
-// query head j to (M, L) in LDS; then every thread combines four channels:
-// out = sum_s o_s exp2(m_s - M) / L (log2 domain).
-__global__ void __launch_bounds__(256) merge_kernel(const dc_merge_item* __restrict__ merges, const float* part_o,
-                                                    const float* part_ml, float* out, int32_t n_kv_heads,
-                                                    int32_t nq, int32_t hd, int64_t max_partials) {
-  __shared__ float sM[kMaxQ], sL[kMaxQ];
+// One wavefront per (merge item, query head j): the lanes reduce the
+// partials' (m, l) to (M, L), then each lane combines four channels,
+// out = sum_s o_s exp2(m_s - M) / L (log2 domain), four partials in flight.
+__global__ void __launch_bounds__(64) merge_kernel(const dc_merge_item* __restrict__ merges, const float* part_o,
+                                                   const float* part_ml, float* out, int32_t n_kv_heads,
+                                                   int32_t nq, int32_t hd, int64_t max_partials) {
   const dc_merge_item mi = merges[blockIdx.x];
+  const int j = blockIdx.y, lane = threadIdx.x;
   if (mi.partial_begin < 0 || mi.count <= 0 || int64_t(mi.partial_begin) + mi.count > max_partials) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const float* ml = part_ml + int64_t(mi.partial_begin) * nq * 2;
-  for (int j = wave; j < nq; j += blockDim.x >> 6) {
-    float M = -INFINITY;
-    for (int s = lane; s < mi.count; s += 64) M = fmaxf(M, ml[(int64_t(s) * nq + j) * 2]);
-    M = wave_max(M);
-    float L = 0.f;
-    for (int s = lane; s < mi.count; s += 64) {
-      const float m = ml[(int64_t(s) * nq + j) * 2];
-      L += m == -INFINITY ? 0.f : ml[(int64_t(s) * nq + j) * 2 + 1] * exp2f(m - M);
-    }
-    L = wave_sum(L);
-    if (lane == 0) {
-      sM[j] = M;
-      sL[j] = L;
-    }
+  const float* ml = part_ml + (int64_t(mi.partial_begin) * nq + j) * 2;  // partial s at ml[2 nq s]
+  float M = -INFINITY;
+  for (int s = lane; s < mi.count; s += 64) M = fmaxf(M, ml[int64_t(s) * nq * 2]);
+  M = wave_max(M);
+  float L = 0.f;
+  for (int s = lane; s < mi.count; s += 64) {
+    const float m = ml[int64_t(s) * nq * 2];
+    L += m == -INFINITY ? 0.f : ml[int64_t(s) * nq * 2 + 1] * exp2f(m - M);
   }
-  __syncthreads();
-  const float* po = part_o + int64_t(mi.partial_begin) * nq * hd;
-  float* o = out + (int64_t(mi.seq) * n_kv_heads + mi.kv_head) * nq * hd;
-  if ((hd & 3) == 0 && ((reinterpret_cast<uintptr_t>(po) | reinterpret_cast<uintptr_t>(o)) & 15) == 0) {
-    // four channels of one head per thread, 16-byte accesses
-    for (int idx = 4 * threadIdx.x; idx < nq * hd; idx += 4 * blockDim.x) {
-      const int j = idx / hd;
-      const float M = sM[j];
+  const float inv = 1.f / fmaxf(wave_sum(L), 1e-30f);
+  const float* po = part_o + (int64_t(mi.partial_begin) * nq + j) * hd;  // partial s at po[nq hd s]
+  float* o = out + ((int64_t(mi.seq) * n_kv_heads + mi.kv_head) * nq + j) * hd;
+  const int64_t step = int64_t(nq) * hd;
+  if ((hd & 3) == 0 && ((reinterpret_cast<uintptr_t>(po) | reinterpret_cast<uintptr_t>(o) | uintptr_t(step * 4)) & 15) == 0) {
+    for (int c = 4 * lane; c < hd; c += 256) {
       float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
       for (int s = 0; s < mi.count; ++s) {
-        const float m = ml[(int64_t(s) * nq + j) * 2];
+        const float m = ml[int64_t(s) * nq * 2];
         const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-        const float4 v = *reinterpret_cast<const float4*>(po + int64_t(s) * nq * hd + idx);
+        const float4 v = *reinterpret_cast<const float4*>(po + s * step + c);
         acc.x += v.x * w;
         acc.y += v.y * w;
         acc.z += v.z * w;
         acc.w += v.w * w;
       }
-      const float inv = 1.f / fmaxf(sL[j], 1e-30f);
-      *reinterpret_cast<float4*>(o + idx) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+      *reinterpret_cast<float4*>(o + c) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
     }
   } else {
-    for (int idx = threadIdx.x; idx < nq * hd; idx += blockDim.x) {
-      const int j = idx / hd;
-      const float M = sM[j];
+    for (int c = lane; c < hd; c += 64) {
       float acc = 0.f;
+#pragma unroll 4
       for (int s = 0; s < mi.count; ++s) {
-        const float m = ml[(int64_t(s) * nq + j) * 2];
-        acc += m == -INFINITY ? 0.f : po[int64_t(s) * nq * hd + idx] * exp2f(m - M);
+        const float m = ml[int64_t(s) * nq * 2];
+        acc += m == -INFINITY ? 0.f : po[s * step + c] * exp2f(m - M);
       }
-      o[idx] = acc / fmaxf(sL[j], 1e-30f);
+      o[c] = acc * inv;
     }
   }
 }
@@ -270,7 +259,7 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
 
 int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream) {
   if (n_merges <= 0) return DC_OK;
-  hipLaunchKernelGGL(merge_kernel, dim3(uint32_t(n_merges)), dim3(256), 0, stream, merges,
+  hipLaunchKernelGGL(merge_kernel, dim3(uint32_t(n_merges), uint32_t(a.n_q)), dim3(64), 0, stream, merges,
                      a.part_o, a.part_ml, a.out, a.n_kv_heads, a.n_q, a.kpool.geometry.head_dim, a.max_partials);
   return check_hip(hipGetLastError(), "merge_kernel launch");
 }
@@ -330,6 +319,28 @@ extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_
 
   int rc = dc::launch_decode(a, hipStream_t(stream));
   if (rc) return rc;
+  return dc::launch_merge(a, merges, n_merges, hipStream_t(stream));
+}
+
+extern "C" int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const void* workspace,
+                            int64_t workspace_bytes, int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, int32_t head_dim,
+                            float* out, dc_stream_t stream) {
+  if (n_merges < 0 || n_seqs <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim > dc::kMaxHD)
+    return dc::fail(DC_EINVAL, "dc_lse_merge: bad sizes");
+  if (n_q <= 0 || n_q > dc::kMaxQ) return dc::fail(DC_EINVAL, "n_q must be in [1, %d]", dc::kMaxQ);
+  if (n_merges == 0) return DC_OK;
+  if (!merges || !out) return dc::fail(DC_EINVAL, "dc_lse_merge: null pointer");
+  const int64_t per_partial = int64_t(n_q) * (head_dim + 2) * 4;
+  const int64_t n_partials = workspace_bytes / per_partial;
+  if (!workspace || n_partials <= 0) return dc::fail(DC_ESPACE, "dc_lse_merge: no partials in the workspace");
+  dc::DecodeArgs a{};
+  a.n_kv_heads = n_kv_heads;
+  a.n_q = n_q;
+  a.out = out;
+  a.kpool.geometry.head_dim = head_dim;
+  a.part_o = reinterpret_cast<float*>(const_cast<void*>(workspace));
+  a.part_ml = a.part_o + n_partials * n_q * head_dim;
+  a.max_partials = n_partials;
   return dc::launch_merge(a, merges, n_merges, hipStream_t(stream));
 }
 

@@ -112,6 +112,7 @@ def decode_paged(
     workspace=None,
     validate: bool = True,
     v_pool: DevicePagePool | None = None,
+    merge: bool = True,
 ):
     """Fused decode for ``queries [n_seqs, n_kv_heads, n_q, head_dim]``.
 
@@ -120,7 +121,9 @@ def decode_paged(
 
     Returns ``out`` fp32 ``[n_seqs, n_kv_heads, n_q, head_dim]``.
     ``seq_pages[b]`` is the number of pages of sequence b (the first
-    entries of its page-table rows).
+    entries of its page-table rows).  ``merge=False`` leaves the split-K
+    partials in ``workspace`` for :func:`merge_partials` (sequences that
+    were not split are written to ``out`` either way).
     """
     torch = _torch()
     vpool = pool if v_pool is None else v_pool
@@ -163,10 +166,22 @@ def decode_paged(
     st = _lib.lib().dc_decode_paged(
         pool.c_pool(), vpool.c_pool(), C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
         C.c_void_p(plan.items.data_ptr()), plan.n_items,
-        C.c_void_p(plan.merges.data_ptr() if plan.merges is not None else 0), plan.n_merges,
+        C.c_void_p(plan.merges.data_ptr() if plan.merges is not None and merge else 0), plan.n_merges if merge else 0,
         C.c_void_p(queries.data_ptr()), dtype_code(queries), float(query_scale), B, H, Q,
         C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()), int(workspace.numel()),
         C.c_void_p(current_stream_ptr()),
     )
     _lib.check(st, "dc_decode_paged")
     return out
+
+
+def merge_partials(plan: DecodePlan, out, workspace) -> None:
+    """The split-K log-sum-exp merge of ``plan`` on its own
+    (``dc_lse_merge``): partials in ``workspace`` -> ``out``."""
+    if plan.n_merges == 0:
+        return
+    B, H, Q, hd = (int(x) for x in out.shape)
+    st = _lib.lib().dc_lse_merge(C.c_void_p(plan.merges.data_ptr()), plan.n_merges, C.c_void_p(workspace.data_ptr()),
+                                 int(workspace.numel()), B, H, Q, hd, C.c_void_p(out.data_ptr()),
+                                 C.c_void_p(current_stream_ptr()))
+    _lib.check(st, "dc_lse_merge")

@@ -14,7 +14,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib
-from .decode import DecodePlan, decode_paged, make_plan, workspace_bytes
+from .decode import DecodePlan, decode_paged, make_plan, merge_partials, workspace_bytes
 from .page_pool import DevicePagePool, PoolGeometry
 
 
@@ -128,6 +128,7 @@ class Workload:
     k_page_ids_by_layer: list = field(default_factory=list)
     v_page_ids_by_layer: list = field(default_factory=list)
     attended: np.ndarray | None = None
+    graph: object = None  # captured HIP graph of one whole step
     tail_k_dev: list = field(default_factory=list)
     tail_v_dev: list = field(default_factory=list)
     slot_dev: object = None
@@ -155,18 +156,53 @@ class Workload:
         """Context tokens each sequence attends per layer (after any append)."""
         return self.attended
 
-    def step(self, layer_hook=None) -> None:
-        """One decode step: per layer, (append) + one fused decode launch."""
-        for l, lt in enumerate(self.layers):
-            if self.spec.append:
-                self._append(l)
-            if layer_hook is not None:
-                layer_hook(l, "begin")
-            decode_paged(self.k_pool, lt.k_table, lt.v_table, lt.seq_pages, self.queries[l],
-                         query_scale=self.query_scale, plan=self.plan, out=self.outs[l], workspace=self.workspace,
-                         validate=False, v_pool=self.v_pool)
-            if layer_hook is not None:
-                layer_hook(l, "end")
+    def step(self) -> None:
+        """One decode step: per layer, (append) + the fused decode kernel +
+        the split-K merge kernel.  Replays the captured graph when
+        :meth:`capture` has been called."""
+        if self.graph is not None:
+            self.graph.replay()
+            return
+        for l in range(len(self.layers)):
+            self.decode_layer(l)
+            self.merge_kernel(l)
+
+    def decode_layer(self, l: int) -> None:
+        """(Append and) the decode kernel of layer ``l``, partials left in
+        the workspace for the merge."""
+        if self.spec.append:
+            self._append(l)
+        self.decode_kernel(l)
+
+    def merge_kernel(self, l: int) -> None:
+        merge_partials(self.plan, self.outs[l], self.workspace)
+
+    def decode_kernel(self, l: int) -> None:
+        """Layer ``l``'s decode kernel alone (``dc_decode_paged`` without
+        the merge)."""
+        lt = self.layers[l]
+        decode_paged(self.k_pool, lt.k_table, lt.v_table, lt.seq_pages, self.queries[l],
+                     query_scale=self.query_scale, plan=self.plan, out=self.outs[l], workspace=self.workspace,
+                     validate=False, v_pool=self.v_pool, merge=False)
+
+    def capture(self) -> None:
+        """Capture one whole step (every layer's append, decode and merge
+        kernels) as a HIP graph; :meth:`step` then replays it, so a decode
+        loop costs one host launch per step.  Pools, tables, plan and
+        buffers must not be reallocated afterwards."""
+        torch = _torch()
+        self.graph = None
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up: descriptor tables and plan uploaded before capture
+            self.step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        torch.cuda.synchronize()
+        self.graph = g
 
     def _append(self, l: int) -> None:
         """Encode this step's new K / V row of every (sequence, KV head) into

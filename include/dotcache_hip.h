@@ -219,6 +219,17 @@ int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, cons
 
 int64_t dc_decode_workspace_bytes(int32_t n_partials, int32_t n_q, int32_t head_dim);
 
+/* The split-K merge on its own: for every merge item, combine partials
+ * [partial_begin, partial_begin + count) of the workspace by log-sum-exp into
+ * out [n_seqs, n_kv_heads, n_q, head_dim].  dc_decode_paged with
+ * n_merges = 0 writes the partials and leaves the merge to this call, which
+ * lets a caller time or schedule the two kernels apart.  Workspace layout and
+ * size as for dc_decode_paged.  Replaces the chunked (m, l) rescale-and-merge
+ * of reference dotcache/backends/torch_mps.py:4276-4435 (the online-softmax
+ * combine across chunks). */
+int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const void* workspace, int64_t workspace_bytes,
+                 int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, int32_t head_dim, float* out, dc_stream_t stream);
+
 /* Process-wide decode kernel choice: 0 (default) runs the MFMA kernel when
  * every page format, head_dim (64/128/256), group size and n_q <= 8 fit it
  * and the generic kernel otherwise; 1 always runs the generic kernel (for
