@@ -52,6 +52,21 @@ def parse():
     return ap.parse_args()
 
 
+def profiled_traffic(workload: str, pages_per_split: int, decode_path: str):
+    """HBM bytes per decode launch measured for this workload by the
+    FETCH_SIZE / WRITE_SIZE runs summarised under profiles/ (calibrated
+    against a copy of known size there), or None if none matches."""
+    import re
+
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        for m in re.finditer(r"<!-- traffic (\{.*?\}) -->", f.read_text()):
+            rec = json.loads(m.group(1))
+            if (rec.get("workload"), rec.get("pages_per_split"), rec.get("decode_path")) == (
+                    workload, pages_per_split, decode_path):
+                return float(rec["traffic_bytes"])
+    return None
+
+
 def copy_probe(nbytes: int) -> None:
     import torch
 
@@ -64,21 +79,22 @@ def copy_probe(nbytes: int) -> None:
 
 
 def cpu_baseline(wl, budget_s: float) -> dict:
-    """Time the CPU oracle (numpy restatement of the reference cpu_ref path)
-    on a bounded sample of the same workload: layer 0, sequence 0, all KV
-    heads, as many GQA query heads as fit in ``budget_s``.  One (sequence,
-    layer, token) position covers every query head, so the rate is
-    tokens x (query heads done / query heads) / seconds."""
+    """Time the CPU oracle (numpy restatement of the reference cpu_ref path:
+    per page score, one global softmax, per page mix, one query head at a
+    time) on a bounded sample of the same workload: layer 0, (sequence, KV
+    head) streams in order, every GQA query head of each, until
+    ``budget_s`` of CPU time is spent.  One (sequence, layer, token)
+    position covers all KV heads, so the rate is tokens of the streams done
+    / KV heads / seconds (the per-token cost is linear in the context, so
+    the sample extrapolates per token position)."""
     from threadpoolctl import threadpool_limits
 
     from oracle import dotcache_oracle as O
 
     spec = wl.spec
     lt = wl.layers[0]
-    n = int(lt.seq_pages[0])
-    kt = lt.k_table[0].cpu().numpy()
-    vt = lt.v_table[0].cpu().numpy()
-    q_all = wl.queries[0][0].float().cpu().numpy() * wl.query_scale  # [H, Q, hd]
+    H, Q = spec.n_kv_heads, spec.gqa
+    q_all = wl.queries[0].float().cpu().numpy() * wl.query_scale  # [B, H, Q, hd]
 
     def to_oracle(pool, pid, kind):
         page = pool.download_page(int(pid), kind=kind)
@@ -86,29 +102,36 @@ def cpu_baseline(wl, budget_s: float) -> dict:
         return O.OraclePage(header=oh, payload=page.payload, scales=page.scales, bias=page.bias,
                             escape_payload=page.escape_payload, escape_scales=page.escape_scales)
 
-    H, Q = spec.n_kv_heads, spec.gqa
-    kp = [[to_oracle(wl.k_pool, kt[h, p], "K") for p in range(n)] for h in range(H)]
-    vp = [[to_oracle(wl.v_pool, vt[h, p], "V") for p in range(n)] for h in range(H)]
-    tokens = int(sum(p.header.token_count for p in kp[0]))
-    done = 0
+    tokens = 0
+    streams = 0
+    dt = 0.0
     with threadpool_limits(limits=1):
-        t0 = time.perf_counter()
-        for j in range(Q):
+        for b in range(spec.batch):
+            n = int(lt.seq_pages[b])
+            kt = lt.k_table[b].cpu().numpy()
+            vt = lt.v_table[b].cpu().numpy()
             for h in range(H):
-                O.decode_step(q_all[h, j], kp[h], vp[h])
-            done += 1
-            if time.perf_counter() - t0 > budget_s:
+                kp = [to_oracle(wl.k_pool, kt[h, p], "K") for p in range(n)]
+                vp = [to_oracle(wl.v_pool, vt[h, p], "V") for p in range(n)]
+                t0 = time.perf_counter()
+                for j in range(Q):
+                    O.decode_step(q_all[b, h, j], kp, vp)
+                dt += time.perf_counter() - t0
+                tokens += sum(p.header.token_count for p in kp)
+                streams += 1
+                if dt > budget_s:
+                    break
+            if dt > budget_s:
                 break
-        dt = time.perf_counter() - t0
-    rate = tokens * done / Q / dt
+    rate = tokens / H / dt
     return {
         "value": rate,
         "unit": "KV tokens/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"layer 0, sequence 0, {H} KV heads x {done}/{Q} query heads over {tokens} tokens "
-                  f"({n} pages) in {dt:.1f} s; numpy oracle of reference cpu_ref (BLAS pinned to 1 thread); "
-                  f"host {os.cpu_count()} cpus",
+        "sample": f"layer 0: {streams} (sequence, KV head) streams x {Q} query heads, {tokens} tokens, "
+                  f"{dt:.1f} s of oracle time (page downloads excluded); numpy oracle of reference cpu_ref, "
+                  f"BLAS pinned to 1 thread; host reports {os.cpu_count()} cpus",
     }
 
 
@@ -116,7 +139,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU). "
-              "The path shards by (sequence, KV head) with no exchange, see DESIGN.md.", file=sys.stderr)
+              "The path shards by (sequence, KV head) with no exchange between GPUs.", file=sys.stderr)
         sys.exit(2)
     import torch
 
@@ -232,7 +255,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": profiled_traffic(spec.name, wl.plan.pages_per_split, args.decode_path),
             "kernel": ("decode_mfma_kernel" if args.decode_path == "auto" else "decode_generic_kernel")
                       + " (dc_decode_paged, one launch per layer)",
             "launch_us": launch_ms * 1e3,

@@ -4,8 +4,8 @@
 ``BackendName`` here is ``"hip_mi355x"`` or ``"auto"``.  ``auto`` resolves
 to ``hip_mi355x`` when a GPU and the library are present and otherwise raises
 RuntimeError: this package ships no CPU path (the reference keeps its own
-``cpu_ref``; ``INTEGRATION.md`` shows how the reference's
-``_resolve_backend`` adds ``hip_mi355x`` next to it).  Errors follow the
+``cpu_ref``, and its ``_resolve_backend`` gains a ``hip_mi355x`` branch next
+to it).  Errors follow the
 reference: RuntimeError for an unavailable device, ValueError for an
 unsupported page or bad shapes.
 """
