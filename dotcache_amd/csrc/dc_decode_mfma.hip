@@ -1,44 +1,45 @@
 // MFMA fast path of the fused paged decode (gfx950, v_mfma_f32_16x16x32_f16).
 //
-// One wavefront runs one work item: it walks its pages, scores the page's
-// tokens for the GQA query heads of its KV head, folds them into a running
-// (max, sum) per head, and mixes the value page -- all from the compressed
-// page bytes.  Accepted pages: keys M3 fp16 or M0 4-bit (group 32, affine or
-// symmetric); values M0 4- or 8-bit (group 32 or 64, affine or symmetric) or
-// M3 fp16.  Other formats take the generic kernel (dc_decode.hip).
+// One wavefront -- one workgroup -- runs one work item: it walks the item's
+// pages in order, scores each 32-token chunk for the GQA query heads of its
+// KV head, folds the logits into a running (max, sum) per head and mixes the
+// value codes, all from the compressed page bytes.  At the end it writes the
+// normalised output (an item that covers its whole sequence) or a split-K
+// partial (m, l, o) for the merge kernel.  Accepted pages: keys M3 fp16 or
+// M0 4-bit (group 32, affine or symmetric); values M0 4- or 8-bit (group 32
+// or 64, affine or symmetric) or M3 fp16; up to 16 query heads per KV head.
+// Other formats take the generic kernel (dc_decode.hip).
 //
 // Exactness.  Every MFMA operand is exact: escape rows are fp16 already,
-// codes (c - zero point) are small integers, and the fp32 operands (scaled
-// queries, softmax weight x value scale) are split into an fp16 high part
-// and an fp16 residual, so each product is an exact fp16 x fp16 product
-// accumulated in fp32.  Per-(token, group) scales and biases are applied in
-// fp32 outside the MFMA, in the reference's streaming form
+// codes minus zero point are small integers, and each fp32 operand (scaled
+// query, softmax weight x value scale) is carried as two fp16 operands, its
+// high part and its residual, each multiplied by the same exact other
+// operand and accumulated in fp32.  Per-(token, group) key scales and biases
+// are applied in fp32 after the MFMA, in the reference's streaming form
 // s * (codes . q_g) + b * sum(q_g) (reference
 // dotcache/attention_reference.py:101-126, :168-192).
 //
-// Pages are processed in chunks of 32 tokens: stage the chunk's value codes
-// and scales in LDS, score it (two 16-token MFMA tiles), update the running
-// max / sum, mix it.  Lane maps (lane l, r = l % 16, kb = l / 16; a
-// 16x16x32 MFMA gives lane l row r of A, column r of B and the D values of
+// Lane maps (lane l, r = l % 16, kb = l / 16; a 16x16x32 MFMA gives lane l
+// row r of A, column r of B, k-slots 8 kb .. 8 kb + 7, and the D values of
 // rows 4 kb + i, column r):
-//   score  D[token, q] = K[token, :] . Q[q, :]   (A = key rows, B = queries).
-//          Tile hh, A row m is chunk token 8 (m / 4) + 4 hh + m % 4, so the
-//          D rows a lane holds are chunk tokens 8 kb + e, e < 8 -- the same
-//          tokens the lane feeds as A k-slots of the mix, so a softmax weight
-//          never leaves the lane that produced it except for the row shuffle
-//          to the residual rows.
-//   mix    D[qrow, d] = A[qrow, token] x B[token, d]; qrow < n_q is the high
-//          part of query head qrow, n_q <= qrow < 2 n_q the residual of head
-//          qrow - n_q; the two rows are added once at the end.  Column r of
-//          tile h of value group g is channel VGS g + 8 (r / L) + r % L + L h
-//          with L = 128 / VGS, which lets every lane unpack its codes with one
-//          byte permute per pair of tokens.
+//   score  D[token, q] = K[token, :] . Q[q, :]  (A = key rows, B = queries,
+//          one MFMA per 32 channels).  In tile hh, A row m is chunk token
+//          8 (m / 4) + 4 hh + m % 4, so lane (r, kb) ends up with the logits
+//          of chunk tokens 8 kb + e, e < 8, for head r.
+//   mix    D[q, d] = A[q, token] x B[token, d]  (A = weights, k = tokens).
+//          Lane (r, kb) feeds A row r = head r at k-slots = chunk tokens
+//          8 kb + e: exactly the logits it holds, so weights never cross
+//          lanes.  Column r of tile h of value group g is channel
+//          VGS g + 8 (r / L) + r % L + L h with L = 128 / VGS, which lets
+//          every lane unpack its codes with one byte permute per pair of
+//          tokens.
 #include "dc_common.h"
 #include "dc_decode.h"
 
 namespace dc {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -51,124 +52,143 @@ __device__ __forceinline__ f32x4 mfma(const Frag& a, const Frag& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, b.h, c, 0, 0, 0);
 }
 
+// Page bytes are read once per launch: nontemporal loads stream them past
+// the caches, which measures about 12 % more HBM read bandwidth on gfx950
+// than ordinary loads for the same access pattern.
+template <typename T>
+__device__ __forceinline__ T stream_load(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+
+__device__ __forceinline__ uint32_t bits_of(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 h2_of(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
 // fp16 pair (lo, hi) from two floats, round to nearest even.
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-  const _Float16 a = (_Float16)lo, b = (_Float16)hi;
-  return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) { return bits_of(h2{(_Float16)lo, (_Float16)hi}); }
+
+// Two fp32 values as their fp16 high parts rtz(x) and fp16 residuals
+// rtz(x - rtz(x)); x - rtz(x) is exact in fp32, so the pair carries x to
+// about 2^-22 relative.
+struct Split2 {
+  uint32_t hi, res;
+};
+// neg1 is -1 held in a register the compiler cannot see through, so
+// x - hi stays one fma with an fp16 operand (v_fma_mix_f32) instead of a
+// conversion and a subtraction.
+__device__ __forceinline__ Split2 split2(float x0, float x1, float neg1) {
+  const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+  const float r0 = __builtin_fmaf(neg1, float(hi[0]), x0), r1 = __builtin_fmaf(neg1, float(hi[1]), x1);
+  return {bits_of(hi), __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1))};
 }
 
-// fp32 -> fp16 high part, or the fp16 residual x - f32(f16(x)).
-__device__ __forceinline__ float split_part(float x, bool residual) {
-  const float hi = float((_Float16)x);
-  return residual ? x - hi : x;
-}
-
-// Packed fp16 pair (1024 + a, 1024 + b) -> (a - z, b - z), exact.
-__device__ __forceinline__ uint32_t magic_sub(uint32_t x, uint32_t neg_bias_pair) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const h2 v = __builtin_bit_cast(h2, x) + __builtin_bit_cast(h2, neg_bias_pair);
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-__device__ __forceinline__ uint32_t h2_const(float v) { return pack_h2(v, v); }
-
-// fp16 bits (low 16 bits of x) -> float
-__device__ __forceinline__ float h2f(uint32_t x) { return float(__builtin_bit_cast(_Float16, uint16_t(x))); }
-
-// Two fp32 values as packed fp16: their high parts rtz(x) (res_neg = 0) or
-// their residuals rtz(x - rtz(x)) (res_neg = -1).  x - rtz(x) is exact in
-// fp32, so high part + residual carries x to about 2^-20 relative.
-__device__ __forceinline__ uint32_t split_pair(float x0, float x1, float res_neg) {
-  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-  const h2v hi = __builtin_bit_cast(h2v, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-  const float r0 = fmaf(float(hi[0]), res_neg, x0);
-  const float r1 = fmaf(float(hi[1]), res_neg, x1);
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
-}
-
-constexpr int kWaves = 4;  // waves per workgroup; each walks its own pages of the work item
+// Weights are exp2(logit - m_ref), with m_ref the head's running max when it
+// last moved; it moves only when a chunk's max exceeds it by more than this
+// (log2 units), so weights stay <= 2^kLazy and the accumulators are rescaled
+// rarely.
+constexpr float kLazy = 2.f;
 
 // Key-page mix of a pool: only M3 rows, only M0 4-bit codes, or both.
 enum KeyMode { KEYS_M3 = 0, KEYS_M0 = 1, KEYS_MIXED = 2 };
 
 template <int HD, int VGS, int VBITS>
 struct MfmaCfg {
-  static constexpr int KG = HD / 32;        // key groups of 32 channels (= contraction steps of the score)
-  static constexpr int VG = HD / VGS;       // value groups
-  static constexpr int H = VGS / 16;        // mix column tiles per value group
-  static constexpr int LPW4 = 128 / VGS;    // lanes sharing one 4-bit code word
-  static constexpr int NACC = VG * H;       // = HD / 16 accumulator tiles
-  static constexpr int W = VBITS == 8 ? VGS / 4 : VGS / 8;  // code words per (token, value group)
-  static constexpr int NVP = VG * 8 * W / 64;                // 16-byte value-code pieces per lane per chunk
-  static constexpr int NKS = (16 * KG + 63) / 64;            // key scale words per lane per chunk
-  static constexpr int NVS = (16 * VG + 63) / 64;            // value scale words per lane per chunk
-  // per-wave LDS: chunk staging -- value codes [VG][32][W], value scales /
-  // biases and key scales / biases transposed to [group][32 tokens] fp16 --
-  // later reused for the end-of-item rows
-  static constexpr int VPAY = VG * 32 * W;
-  static constexpr int VSC = VPAY, VBS = VSC + 16 * VG, KSC = VBS + 16 * VG, KBS = KSC + 16 * KG;
-  static constexpr int STAGE = KBS + 16 * KG;
-  static constexpr int ROWS = 16 * HD + 16 * VG;  // D rows of the mix + bias sums
-  static constexpr int WAVE_WORDS = STAGE > ROWS ? STAGE : ROWS;
-  static constexpr int LDS_WORDS = kWaves * WAVE_WORDS;
+  static constexpr int KG = HD / 32;          // key groups of 32 channels (= contraction steps of the score)
+  static constexpr int VG = HD / VGS;         // value groups
+  static constexpr int H = VGS / 16;          // mix column tiles per value group
+  static constexpr int LPW4 = 128 / VGS;      // lanes sharing one code word
+  static constexpr int NACC = HD / 16;        // mix accumulator tiles
+  static constexpr int W = VBITS * VGS / 32;  // code words per (token, value group)
+  // LDS staging of a chunk's value codes: per group 32 tokens of W words with
+  // W pad words after every 8 tokens, so the words that the lanes of one read
+  // touch fall in distinct banks
+  static constexpr int PAD = W;
+  static constexpr int GSTRIDE = 32 * W + 4 * PAD;
+  static constexpr int NVP = VG * 8 * W / 64;  // 16-byte code pieces per lane per chunk
+  static constexpr int VSW = 16 * VG;          // value scale words per chunk ([32][VG] fp16)
+  static constexpr int KSW = 16 * KG;          // key scale words per chunk ([32][KG] fp16)
+  static constexpr int NVS = (VSW + 63) / 64;
+  static constexpr int NKS = (KSW + 63) / 64;
+  static constexpr int VPAY = 0, VSC = VG * GSTRIDE, VBS = VSC + VSW, KSC = VBS + VSW, KBS = KSC + KSW;
+  static constexpr int LDS_WORDS = KBS + KSW;
   static_assert(VG * 8 * W % 64 == 0, "value pieces must spread evenly over the wave");
+  static_assert(W % 4 == 0, "value code rows are staged in 16-byte pieces");
 };
 
 // Registers one chunk needs from HBM.  The next chunk's loads are issued
-// into them as soon as the current chunk has consumed them (values and
-// scales after staging, keys after the score), so they are in flight during
-// its mix.  Every chunk issues the same loads whatever its page formats, so
-// the compiler never has to drain the queue to merge register versions.
-template <int HD, int VGS, int VBITS>
+// into them while the current chunk is scored and mixed.  Every chunk issues
+// the same loads whatever its page formats, so the compiler never has to
+// drain the queue to merge register versions.
+template <int HD, int VGS, int VBITS, int KMODE>
 struct ChunkRegs {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  u32x4 kr[2][Cfg::KG];  // key rows (M3: 8 fp16) or the 16-byte code block of (token, group) (M0)
-  u32x4 vr[Cfg::NVP];    // value code pieces, blob byte order
+  static constexpr bool kWordKeys = KMODE == KEYS_M0;
+  // keys: M3 row pieces (8 fp16) or the 16-byte code block of (token, group);
+  // a pool of M0 keys only needs this lane's word of that block
+  u32x4 kr[kWordKeys ? 1 : 2][kWordKeys ? 1 : Cfg::KG];
+  uint32_t kw[kWordKeys ? 2 : 1][kWordKeys ? Cfg::KG : 1];
+  u32x4 vr[Cfg::NVP];  // value code pieces, blob byte order
   uint32_t ks[Cfg::NKS], kbw[Cfg::NKS], vs[Cfg::NVS], vb[Cfg::NVS];  // scale / bias words
 };
 
+// One chunk: the page it belongs to (wave-uniform, in SGPRs) and its first token.
 struct PageMeta {
+  __amdgpu_buffer_rsrc_t krs, vrs;  // buffer resources of the key / value blobs
   const uint8_t* kp;
   const uint8_t* vp;
-  int T;  // tokens to read (0: skip the page)
-  int kfmt, vfmt, vbits;
+  int T;  // tokens of the page
+  int kfmt, vfmt;
   uint32_t ksc, kbs, vsc, vbs;  // byte offsets of scales / biases in the blobs (0 where absent)
+  int c0;                       // first token of the chunk
 };
 
 template <int HD, int VGS, int KMODE, int VBITS, bool VM3>
-__global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(DecodeArgs a) {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  using Regs = ChunkRegs<HD, VGS, VBITS>;
-  constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W;
-  __shared__ uint32_t lds_all[Cfg::LDS_WORDS];
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  using Regs = ChunkRegs<HD, VGS, VBITS, KMODE>;
+  constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W, NACC = Cfg::NACC;
+  __shared__ uint32_t lds[Cfg::LDS_WORDS];
 
   const dc_work_item it = a.items[blockIdx.x];
-  // readfirstlane tells the compiler the wave index is uniform, so page and
-  // chunk loop state, blob pointers and page metadata live in SGPRs
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int lane = threadIdx.x;
   const int r = lane & 15, kb = lane >> 4;
   const int nq = a.n_q;
   const int CAP = a.kpool.geometry.page_capacity;
-  uint32_t* lds = lds_all + wave * Cfg::WAVE_WORDS;
-  uint16_t* vsc = reinterpret_cast<uint16_t*>(lds + Cfg::VSC);
-  uint16_t* vbs = reinterpret_cast<uint16_t*>(lds + Cfg::VBS);
-  uint16_t* ksc = reinterpret_cast<uint16_t*>(lds + Cfg::KSC);
-  uint16_t* kbs = reinterpret_cast<uint16_t*>(lds + Cfg::KBS);
+  const bool head_live = r < nq;
 
-  // ---- queries scaled by query_scale * log2(e); B fragments hi / residual ----
-  // lane (r, kb) holds channels 32 g + 8 kb + i of head r; one vector load per
-  // group.
+  // ---- page metadata: lane i holds the ids / descriptors of page begin + base + i ----
+  const int64_t trow = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * a.table_stride;
+  const int np = it.page_end - it.page_begin;
+  uint32_t k0 = 0, k1 = 0, v0 = 0, v1 = 0;
+  int ok = 0;
+  auto load_meta = [&](int base) {
+    const int nb = np - base < 64 ? np - base : 64;
+    k0 = k1 = v0 = v1 = 0u;
+    ok = 0;
+    if (lane < nb) {
+      const int p = it.page_begin + base + lane;
+      const int kid = a.k_table[trow + p], vid = a.v_table[trow + p];
+      if (kid >= 0 && kid < a.kpool.n_descs && vid >= 0 && vid < a.vpool.n_descs) {
+        const uint2 kd = *reinterpret_cast<const uint2*>(a.kpool.descs + kid);
+        const uint2 vd = *reinterpret_cast<const uint2*>(a.vpool.descs + vid);
+        k0 = kd.x; k1 = kd.y; v0 = vd.x; v1 = vd.y;
+        ok = 1;
+      }
+    }
+  };
+  if (np > 0) load_meta(0);
+
+  // ---- queries scaled by query_scale * log2(e): B fragments hi / residual ----
+  // lane (r, kb) holds channels 32 g + 8 kb + i of head r
   const int64_t qbase = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * nq * HD;
   const float qmul = a.q_scale * kLog2e;
-  const int64_t qrow = qbase + int64_t(r < nq ? r : 0) * HD + 8 * kb;
   Frag qhi[KG], qlo[KG];
   float qsum[KG];
-  auto setup_queries = [&]() {
+  {
+    const int64_t qrow = qbase + int64_t(head_live ? r : 0) * HD + 8 * kb;
     float qv[KG][8];
     if (a.queries_dtype == DC_F32) {
       const float* q = reinterpret_cast<const float*>(a.queries) + qrow;
-  #pragma unroll
+#pragma unroll
       for (int g = 0; g < KG; ++g) {
         const float4 x0 = *reinterpret_cast<const float4*>(q + 32 * g);
         const float4 x1 = *reinterpret_cast<const float4*>(q + 32 * g + 4);
@@ -178,71 +198,67 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
     } else {
       const uint16_t* q = reinterpret_cast<const uint16_t*>(a.queries) + qrow;
       const bool bf = a.queries_dtype == DC_BF16;
-  #pragma unroll
+#pragma unroll
       for (int g = 0; g < KG; ++g) {
         const uint4 x = *reinterpret_cast<const uint4*>(q + 32 * g);
         const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < 4; ++i) {
-          qv[g][2 * i] = bf ? __uint_as_float(xs[i] << 16) : h2f(xs[i] & 0xffffu);
-          qv[g][2 * i + 1] = bf ? __uint_as_float(xs[i] & 0xffff0000u) : h2f(xs[i] >> 16);
+          qv[g][2 * i] = bf ? __uint_as_float(xs[i] << 16) : float(h2_of(xs[i])[0]);
+          qv[g][2 * i + 1] = bf ? __uint_as_float(xs[i] & 0xffff0000u) : float(h2_of(xs[i])[1]);
         }
       }
     }
-  #pragma unroll
+#pragma unroll
     for (int g = 0; g < KG; ++g) {
       float s = 0.f;
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float v0 = r < nq ? qv[g][2 * i] * qmul : 0.f, v1 = r < nq ? qv[g][2 * i + 1] * qmul : 0.f;
-        qhi[g].u[i] = pack_h2(v0, v1);
-        qlo[g].u[i] = pack_h2(split_part(v0, true), split_part(v1, true));
-        s += v0 + v1;
+        const float x0 = head_live ? qv[g][2 * i] * qmul : 0.f, x1 = head_live ? qv[g][2 * i + 1] * qmul : 0.f;
+        qhi[g].u[i] = pack_h2(x0, x1);
+        const h2 hv = h2_of(qhi[g].u[i]);
+        qlo[g].u[i] = pack_h2(x0 - float(hv[0]), x1 - float(hv[1]));
+        s += x0 + x1;
       }
       s += __shfl_xor(s, 16, 64);
       s += __shfl_xor(s, 32, 64);
-      qsum[g] = s;  // sum over group g for head r
+      qsum[g] = s;  // sum of group g of head r
     }
-  };
-
-  // mix A-row role of this lane: high part (r < nq) or residual (nq <= r < 2 nq) of head qa
-  const bool row_live = r < 2 * nq;
-  const bool residual = r >= nq;
-  const int pa_src = kb * 16 + (row_live ? (residual ? r - nq : r) : 0);
-  int rowq[4];  // head of mix D rows 4 kb + i
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * kb + i;
-    rowq[i] = row < nq ? row : (row < 2 * nq ? row - nq : 0);
   }
+
   // mix column of this lane in tile h of value group g: d = VGS g + dcol + LPW4 h
   const int jj = r % LPW4, w4 = r / LPW4;
   const int dcol = 8 * w4 + jj;
-  const float res_neg = residual ? -1.f : 0.f;
   // byte-permute selectors of this lane's code in tile h: the byte of token
-  // 2p into byte 0, of token 2p + 1 into byte 2 (4-bit: byte holding nibble
-  // jj + LPW4 h; 8-bit: byte (jj + LPW4 h) % 4)
+  // 2p into byte 0, of token 2p + 1 into byte 2 (4-bit: the byte of word w4
+  // holding nibble jj + LPW4 h; 8-bit: byte (jj + LPW4 h) % 4 of word
+  // 2 w4 + (jj + LPW4 h) / 4)
   uint32_t vsel[H];
+  int vword[H];
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    const uint32_t b = VBITS == 4 ? uint32_t((jj + LPW4 * h) >> 1) : uint32_t((jj + LPW4 * h) & 3);
+    const int e = jj + LPW4 * h;
+    const uint32_t b = VBITS == 4 ? uint32_t(e >> 1) : uint32_t(e & 3);
     vsel[h] = 0x0c000c00u | b | ((4u + b) << 16);
+    vword[h] = VBITS == 4 ? w4 : 2 * w4 + (e >> 2);
   }
   const uint32_t nib_mask = (jj & 1) ? 0x00f000f0u : 0x000f000fu;  // low or high nibble of the byte
   const h2 nib_mul = (jj & 1) ? h2{(_Float16)0.0625f, (_Float16)0.0625f} : h2{(_Float16)1.f, (_Float16)1.f};
+  // LDS word of (token 8 kb + e, word w) of group g: g GSTRIDE + vrow + e W + w
+  const int vrow = 8 * kb * W + kb * Cfg::PAD;
 
-  f32x4 acc[Cfg::NACC];
+  f32x4 acc[NACC];
 #pragma unroll
-  for (int t = 0; t < Cfg::NACC; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NACC; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float bsum[VG];
 #pragma unroll
   for (int g = 0; g < VG; ++g) bsum[g] = 0.f;
-  float m_run = -INFINITY, l_part = 0.f;
+  float m_ref = -INFINITY, l_part = 0.f;
+  bool any_affine = false;
+  float neg1 = -1.f;
+  asm volatile("" : "+v"(neg1));
 
   const dc_page_geometry kgeo = a.kpool.geometry, vgeo = a.vpool.geometry;
-  const int64_t trow = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * a.table_stride;
-  const int n_item = it.page_end - it.page_begin;
-  const int np = n_item > wave ? (n_item - wave + kWaves - 1) / kWaves : 0;  // pages of this wave
 
   auto key_is_m3 = [&](const PageMeta& m) -> bool {
     if constexpr (KMODE == KEYS_M3) return true;
@@ -254,97 +270,113 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
     return is_m0(m.vfmt);
   };
 
-  // ---- loads of one chunk into registers (the same loads for every format) ----
+  // ---- loads of one chunk into registers ----
+  // Buffer loads against a per-page resource (base = the blob, size = the
+  // blob's bytes, so an access past the page reads zeros instead of another
+  // page): a per-lane offset fixed for the whole item, a wave-uniform chunk
+  // offset and a constant, with no per-chunk address arithmetic in VGPRs.
+  uint32_t koff_m3[2], koff_m0[2];  // A-row token of tile hh: 8 (r / 4) + 4 hh + r % 4
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
+    koff_m3[hh] = (ta * HD + 8 * kb) * 2;                     // M3 row piece, channels 8 kb .. of group 0
+    koff_m0[hh] = ta * 16 + (Regs::kWordKeys ? 4 * kb : 0);  // (token, group 0) code block (or its word kb)
+  }
+  uint32_t voff[Cfg::NVP];
+#pragma unroll
+  for (int k = 0; k < Cfg::NVP; ++k) {
+    const int e = lane + 64 * k;
+    const int g = e / (8 * W), piece = e - g * (8 * W);
+    voff[k] = uint32_t(g * CAP * W * 4 + piece * 16);
+  }
+  const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
+  constexpr int kNT = 2;  // cache policy: nontemporal
   auto load_keys = [&](const PageMeta& m, int c0, Regs& R) {
-    const bool km3 = key_is_m3(m);
+    if constexpr (Regs::kWordKeys) {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int ta = c0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+      for (int g = 0; g < KG; ++g)
 #pragma unroll
-      for (int g = 0; g < KG; ++g) {
-        const int off = km3 ? (ta * HD + 32 * g + 8 * kb) * 2 : (g * CAP + ta) * 16;
-        R.kr[hh][g] = *reinterpret_cast<const u32x4*>(m.kp + off);
+        for (int hh = 0; hh < 2; ++hh)
+          R.kw[hh][g] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(koff_m0[hh]), c0 * 16 + g * CAP * 16, kNT);
+    } else {
+      const bool km3 = key_is_m3(m);
+      const int cbase = c0 * (km3 ? HD * 2 : 16);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint32_t lo = km3 ? koff_m3[hh] : koff_m0[hh];
+#pragma unroll
+        for (int g = 0; g < KG; ++g) {
+          const int goff = km3 ? 64 * g : g * CAP * 16;
+          R.kr[hh][g] = __builtin_amdgcn_raw_buffer_load_b128(m.krs, int(lo), cbase + goff, kNT);
+        }
       }
     }
     if constexpr (KMODE != KEYS_M3) {
-      const uint32_t* S = reinterpret_cast<const uint32_t*>(m.kp + m.ksc) + c0 * KG / 2;
-      const uint32_t* B = reinterpret_cast<const uint32_t*>(m.kp + m.kbs) + c0 * KG / 2;
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
-        const int e = (lane + 64 * k) % (16 * KG);
-        R.ks[k] = S[e];
-        R.kbw[k] = B[e];
+        R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), int(m.ksc) + c0 * KG * 2 + 256 * k, kNT);
+        R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), int(m.kbs) + c0 * KG * 2 + 256 * k, kNT);
       }
     }
   };
   auto load_values = [&](const PageMeta& m, int c0, Regs& R) {
 #pragma unroll
-    for (int k = 0; k < Cfg::NVP; ++k) {
-      const int e = lane + 64 * k;
-      const int g = e / (8 * W), piece = e - g * (8 * W);
-      R.vr[k] = *reinterpret_cast<const u32x4*>(m.vp + (((g * CAP + c0) * W) / 4 + piece) * 16);
-    }
-    const uint32_t* S = reinterpret_cast<const uint32_t*>(m.vp + m.vsc) + c0 * VG / 2;
-    const uint32_t* B = reinterpret_cast<const uint32_t*>(m.vp + m.vbs) + c0 * VG / 2;
+    for (int k = 0; k < Cfg::NVP; ++k) R.vr[k] = __builtin_amdgcn_raw_buffer_load_b128(m.vrs, int(voff[k]), c0 * W * 4, kNT);
 #pragma unroll
     for (int k = 0; k < Cfg::NVS; ++k) {
-      const int e = (lane + 64 * k) % (16 * VG);
-      R.vs[k] = S[e];
-      R.vb[k] = B[e];
+      R.vs[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), int(m.vsc) + c0 * VG * 2 + 256 * k, kNT);
+      R.vb[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), int(m.vbs) + c0 * VG * 2 + 256 * k, kNT);
     }
   };
 
-  // ---- registers -> this wave's LDS staging area ----
+  // ---- registers -> LDS: value codes in padded rows, scales as loaded ([32][G] fp16) ----
   auto stage_chunk = [&](const Regs& R) {
-    u32x4* dst = reinterpret_cast<u32x4*>(lds);
 #pragma unroll
-    for (int k = 0; k < Cfg::NVP; ++k) dst[lane + 64 * k] = R.vr[k];
-    // scale word e holds (token, group) entries 2e and 2e + 1 of the chunk's [32][G] array
+    for (int k = 0; k < Cfg::NVP; ++k) {
+      const int e = lane + 64 * k;
+      const int g = e / (8 * W), piece = e - g * (8 * W);
+      const int t = piece / (W / 4), wc = piece - t * (W / 4);
+      *reinterpret_cast<u32x4*>(lds + Cfg::VPAY + g * Cfg::GSTRIDE + t * W + (t >> 3) * Cfg::PAD + 4 * wc) = R.vr[k];
+    }
 #pragma unroll
     for (int k = 0; k < Cfg::NVS; ++k) {
       const int e = lane + 64 * k;
-      if (e < 16 * VG) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int hidx = 2 * e + s, t = hidx / VG, g = hidx - t * VG;
-          vsc[g * 32 + t] = uint16_t(R.vs[k] >> (16 * s));
-          vbs[g * 32 + t] = uint16_t(R.vb[k] >> (16 * s));
-        }
+      if (Cfg::VSW % 64 == 0 || e < Cfg::VSW) {
+        lds[Cfg::VSC + e] = R.vs[k];
+        lds[Cfg::VBS + e] = R.vb[k];
       }
     }
     if constexpr (KMODE != KEYS_M3) {
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
         const int e = lane + 64 * k;
-        if (e < 16 * KG) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const int hidx = 2 * e + s, t = hidx / KG, g = hidx - t * KG;
-            ksc[g * 32 + t] = uint16_t(R.ks[k] >> (16 * s));
-            kbs[g * 32 + t] = uint16_t(R.kbw[k] >> (16 * s));
-          }
+        if (Cfg::KSW % 64 == 0 || e < Cfg::KSW) {
+          lds[Cfg::KSC + e] = R.ks[k];
+          lds[Cfg::KBS + e] = R.kbw[k];
         }
       }
     }
   };
 
-  // ---- score of one chunk: logits of this lane's chunk tokens 8 kb + e for head r ----
+  // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
   auto score_chunk = [&](const PageMeta& m, const Regs& R, float* Ls) {
     if (key_is_m3(m)) {
+      if constexpr (!Regs::kWordKeys) {
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+        for (int hh = 0; hh < 2; ++hh) {
+          f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int g = 0; g < KG; ++g) {
-          Frag ka;
-          ka.u[0] = R.kr[hh][g].x; ka.u[1] = R.kr[hh][g].y; ka.u[2] = R.kr[hh][g].z; ka.u[3] = R.kr[hh][g].w;
-          d = mfma(ka, qhi[g], d);
-          d = mfma(ka, qlo[g], d);
+          for (int g = 0; g < KG; ++g) {
+            Frag ka;
+            ka.u[0] = R.kr[hh][g].x; ka.u[1] = R.kr[hh][g].y; ka.u[2] = R.kr[hh][g].z; ka.u[3] = R.kr[hh][g].w;
+            d = mfma(ka, qhi[g], d);
+            d = mfma(ka, qlo[g], d);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = d[i];
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = d[i];
       }
-    } else {  // M0 4-bit, group 32: scale and bias applied per group in fp32
+    } else if constexpr (KMODE != KEYS_M3) {  // M0 4-bit, group 32: scale and bias per group in fp32
       const bool k_affine = m.kfmt == DC_FMT_M0_AFFINE;
       const float zp = k_affine ? 0.f : 7.f;
       // (1024 + n_lo, 1024 + 16 n_hi) -> (n_lo - zp, n_hi - zp)
@@ -352,28 +384,42 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
       const h2 kadd = {(_Float16)(-1024.f - zp), (_Float16)(-64.f - zp)};
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
+        // scales / biases of the D-row tokens 8 kb + 4 hh + i, all groups: [4][KG] fp16
+        uint32_t sw[2 * KG], bw[2 * KG];
+#pragma unroll
+        for (int k = 0; k < 2 * KG; k += 4) {
+          const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KSC + (8 * kb + 4 * hh) * KG / 2 + k);
+          sw[k] = s4.x; sw[k + 1] = s4.y; sw[k + 2] = s4.z; sw[k + 3] = s4.w;
+          const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KBS + (8 * kb + 4 * hh) * KG / 2 + k);
+          bw[k] = b4.x; bw[k + 1] = b4.y; bw[k + 2] = b4.z; bw[k + 3] = b4.w;
+        }
         float Lh[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int g = 0; g < KG; ++g) {
-          const uint32_t w = kb == 0 ? R.kr[hh][g].x : kb == 1 ? R.kr[hh][g].y : kb == 2 ? R.kr[hh][g].z : R.kr[hh][g].w;
+          uint32_t w;
+          if constexpr (Regs::kWordKeys) {
+            w = R.kw[hh][g];
+          } else {
+            w = kb == 0 ? R.kr[hh][g].x : kb == 1 ? R.kr[hh][g].y : kb == 2 ? R.kr[hh][g].z : R.kr[hh][g].w;
+          }
           Frag ka;
 #pragma unroll
           for (int p = 0; p < 4; ++p) {
             // byte p holds channel 2p (low nibble) and 2p + 1 (high nibble)
             const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0c040c00u + 0x00010001u * p);
-            const h2 v = __builtin_bit_cast(h2, (x & 0x00f0000fu) | 0x64006400u) * kmul + kadd;
-            ka.u[p] = __builtin_bit_cast(uint32_t, v);
+            ka.u[p] = bits_of(h2_of((x & 0x00f0000fu) | 0x64006400u) * kmul + kadd);
           }
           f32x4 d = {0.f, 0.f, 0.f, 0.f};
           d = mfma(ka, qhi[g], d);
           d = mfma(ka, qlo[g], d);
-          // D rows 4 kb + i are chunk tokens 8 kb + 4 hh + i
-          const uint2 sw = *reinterpret_cast<const uint2*>(ksc + g * 32 + 8 * kb + 4 * hh);
-          const uint2 bw = *reinterpret_cast<const uint2*>(kbs + g * 32 + 8 * kb + 4 * hh);
-          const uint32_t sv[4] = {sw.x & 0xffffu, sw.x >> 16, sw.y & 0xffffu, sw.y >> 16};
-          const uint32_t bv[4] = {bw.x & 0xffffu, bw.x >> 16, bw.y & 0xffffu, bw.y >> 16};
+          // D row 4 kb + i is chunk token 8 kb + 4 hh + i: its (token, g)
+          // entry is half (i KG + g) % 2 of word (i KG + g) / 2
 #pragma unroll
-          for (int i = 0; i < 4; ++i) Lh[i] += h2f(sv[i]) * d[i] + (k_affine ? h2f(bv[i]) * qsum[g] : 0.f);
+          for (int i = 0; i < 4; ++i) {
+            const int e = i * KG + g;
+            Lh[i] += float(h2_of(sw[e >> 1])[e & 1]) * d[i];
+            if (k_affine) Lh[i] += float(h2_of(bw[e >> 1])[e & 1]) * qsum[g];
+          }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = Lh[i];
@@ -383,99 +429,104 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
 
   // ---- online softmax update and mix of one staged chunk ----
   auto mix_chunk = [&](const PageMeta& m, int c0, float* Ls) {
-    // online softmax for head r (the four kb lanes hold its 32 tokens)
-    float mx = -INFINITY;
+    if (c0 + 32 > m.T) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (c0 + 8 * kb + e >= m.T) Ls[e] = -INFINITY;
-      mx = fmaxf(mx, Ls[e]);
+      for (int e = 0; e < 8; ++e)
+        if (c0 + 8 * kb + e >= m.T) Ls[e] = -INFINITY;
     }
+    float mx = Ls[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, Ls[e]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
-    float psum = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      Ls[e] = Ls[e] == -INFINITY ? 0.f : exp2f(Ls[e] - m_new);
-      psum += Ls[e];
-    }
-    l_part = l_part * alpha + psum;
-    m_run = m_new;
-    if (__any(alpha != 1.f)) {
-      float arow[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, rowq[i], 64);
-#pragma unroll
-      for (int t = 0; t < Cfg::NACC; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] *= arow[i];
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // chunk max of head r
+    const bool move = mx > m_ref + kLazy;
+    if (__any(move)) {
+      const float m_new = move ? mx : m_ref;
+      const float alpha = m_ref == -INFINITY ? 0.f : exp2f(m_ref - m_new);
+      m_ref = m_new;
+      l_part *= alpha;
 #pragma unroll
       for (int g = 0; g < VG; ++g) bsum[g] *= alpha;
+      // D row 4 kb + i of the accumulators is head 4 kb + i: its alpha lives in lane 4 kb + i
+      float arow[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * kb + i, 64);
+#pragma unroll
+      for (int t = 0; t < NACC; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] *= arow[i];
     }
-
-    // weights of this lane's A-row head on its 8 tokens
+    // weights of head r on tokens 8 kb + e (0 past the page end and for rows >= n_q)
     float pa[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float v = __shfl(Ls[e], pa_src, 64);
-      pa[e] = row_live ? v : 0.f;
+      const float w = __builtin_amdgcn_exp2f(Ls[e] - m_ref);
+      pa[e] = head_live ? w : 0.f;
+      l_part += pa[e];
     }
     if (value_is_m0(m)) {
       const bool v_affine = m.vfmt == DC_FMT_M0_AFFINE;
+      any_affine = any_affine || v_affine;
       const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
       // codes become fp16 (1024 + c), or (1024 + 16 c) for a code in the high
       // nibble of its byte; one packed fma maps either to c - zp exactly
       const h2 vadd = VBITS == 4 && (jj & 1) ? h2{(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)}
                                               : h2{(_Float16)(-1024.f - zp), (_Float16)(-1024.f - zp)};
+      // scales of tokens 8 kb + e, all groups: [8][VG] fp16 = 4 VG words
+      uint32_t sw[4 * VG];
+#pragma unroll
+      for (int k = 0; k < 4 * VG; k += 4) {
+        const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VSC + 4 * VG * kb + k);
+        sw[k] = s4.x; sw[k + 1] = s4.y; sw[k + 2] = s4.z; sw[k + 3] = s4.w;
+      }
 #pragma unroll
       for (int g = 0; g < VG; ++g) {
-        const uint4 s8 = *reinterpret_cast<const uint4*>(vsc + g * 32 + 8 * kb);
-        const uint32_t sx[4] = {s8.x, s8.y, s8.z, s8.w};
-        Frag fa;
+        Frag fa_hi, fa_res;
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const h2 sv = __builtin_bit_cast(h2, sx[pp]);
-          fa.u[pp] = split_pair(pa[2 * pp] * float(sv[0]), pa[2 * pp + 1] * float(sv[1]), res_neg);
+          const int e0 = (2 * pp) * VG + g, e1 = (2 * pp + 1) * VG + g;  // (token, group) entries
+          // weight x fp16 scale as an fma with a zero addend: one v_fma_mix_f32
+          const float x0 = __builtin_fmaf(pa[2 * pp], float(h2_of(sw[e0 >> 1])[e0 & 1]), 0.f);
+          const float x1 = __builtin_fmaf(pa[2 * pp + 1], float(h2_of(sw[e1 >> 1])[e1 & 1]), 0.f);
+          const Split2 sp = split2(x0, x1, neg1);
+          fa_hi.u[pp] = sp.hi;
+          fa_res.u[pp] = sp.res;
         }
         if (v_affine) {
-          const uint4 b8 = *reinterpret_cast<const uint4*>(vbs + g * 32 + 8 * kb);
-          const uint32_t bx[4] = {b8.x, b8.y, b8.z, b8.w};
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            const h2 bv = __builtin_bit_cast(h2, bx[pp]);
-            bsum[g] += Ls[2 * pp] * float(bv[0]) + Ls[2 * pp + 1] * float(bv[1]);
+            const int e0 = (2 * pp) * VG + g, e1 = (2 * pp + 1) * VG + g;
+            const uint32_t b0 = lds[Cfg::VBS + 4 * VG * kb + (e0 >> 1)];
+            const uint32_t b1 = lds[Cfg::VBS + 4 * VG * kb + (e1 >> 1)];
+            bsum[g] += pa[2 * pp] * float(h2_of(b0)[e0 & 1]) + pa[2 * pp + 1] * float(h2_of(b1)[e1 & 1]);
           }
         }
-        const uint32_t* Pw = lds + (g * 32 + 8 * kb) * W;  // words of tokens 8 kb + e
+        const uint32_t* P = lds + Cfg::VPAY + g * Cfg::GSTRIDE + vrow;  // token 8 kb + e at P[e W]
 #pragma unroll
         for (int h = 0; h < H; ++h) {
           Frag fb;
-          if constexpr (VBITS == 4) {
 #pragma unroll
-            for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t x = __builtin_amdgcn_perm(Pw[(2 * pp + 1) * W + w4], Pw[(2 * pp) * W + w4], vsel[h]);
-              const h2 c = __builtin_bit_cast(h2, (x & nib_mask) | 0x64006400u) * nib_mul + vadd;
-              fb.u[pp] = __builtin_bit_cast(uint32_t, c);
-            }
-          } else {
-            const int wsel = 2 * w4 + ((jj + LPW4 * h) >> 2);  // channel dcol + LPW4 h: word 2 w4 + e / 4, byte e % 4
-#pragma unroll
-            for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t x = __builtin_amdgcn_perm(Pw[(2 * pp + 1) * W + wsel], Pw[(2 * pp) * W + wsel], vsel[h]);
-              const h2 c = __builtin_bit_cast(h2, x | 0x64006400u) + vadd;
-              fb.u[pp] = __builtin_bit_cast(uint32_t, c);
-            }
+          for (int pp = 0; pp < 4; ++pp) {
+            const uint32_t x =
+                __builtin_amdgcn_perm(P[(2 * pp + 1) * W + vword[h]], P[(2 * pp) * W + vword[h]], vsel[h]);
+            if constexpr (VBITS == 4)
+              fb.u[pp] = bits_of(h2_of((x & nib_mask) | 0x64006400u) * nib_mul + vadd);
+            else
+              fb.u[pp] = bits_of(h2_of(x | 0x64006400u) + vadd);
           }
-          acc[g * H + h] = mfma(fa, fb, acc[g * H + h]);
+          acc[g * H + h] = mfma(fa_hi, fb, acc[g * H + h]);
+          acc[g * H + h] = mfma(fa_res, fb, acc[g * H + h]);
         }
-        __builtin_amdgcn_sched_barrier(0);  // keep every group's LDS reads from being hoisted at once
       }
     } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): gather columns from the rows
       const uint16_t* V = reinterpret_cast<const uint16_t*>(m.vp);
-      Frag fa;
+      Frag fa_hi, fa_res;
 #pragma unroll
-      for (int pp = 0; pp < 4; ++pp) fa.u[pp] = split_pair(pa[2 * pp], pa[2 * pp + 1], res_neg);
+      for (int pp = 0; pp < 4; ++pp) {
+        const Split2 sp = split2(pa[2 * pp], pa[2 * pp + 1], neg1);
+        fa_hi.u[pp] = sp.hi;
+        fa_res.u[pp] = sp.res;
+      }
 #pragma unroll
       for (int g = 0; g < VG; ++g)
 #pragma unroll
@@ -489,184 +540,152 @@ __global__ void __launch_bounds__(kWaves * 64, HD >= 256 ? 1 : 2) decode_mfma_ke
             const uint32_t hi = t0 + 1 < m.T ? V[(t0 + 1) * HD + d] : 0u;
             fb.u[pp] = lo | (hi << 16);
           }
-          acc[g * H + h] = mfma(fa, fb, acc[g * H + h]);
+          acc[g * H + h] = mfma(fa_hi, fb, acc[g * H + h]);
+          acc[g * H + h] = mfma(fa_res, fb, acc[g * H + h]);
         }
     }
   };
 
-  // ---- walk this wave's pages: page meta 64 pages at a time, chunks pipelined ----
-  // lane i < nb holds the ids / descriptors of the wave's page base + i; the
-  // first batch is fetched before the query setup so the two overlap
-  uint32_t k0 = 0, k1 = 0, v0 = 0, v1 = 0;
-  int ok = 0;
-  auto load_meta = [&](int base) {
-    const int nb = np - base < 64 ? np - base : 64;
-    k0 = k1 = v0 = v1 = 0u;
-    ok = 0;
-    if (lane < nb) {
-      const int p = it.page_begin + wave + kWaves * (base + lane);
-      const int kid = a.k_table[trow + p], vid = a.v_table[trow + p];
-      if (kid >= 0 && kid < a.kpool.n_descs && vid >= 0 && vid < a.vpool.n_descs) {
-        const uint2 kd = *reinterpret_cast<const uint2*>(a.kpool.descs + kid);
-        const uint2 vd = *reinterpret_cast<const uint2*>(a.vpool.descs + vid);
-        k0 = kd.x; k1 = kd.y; v0 = vd.x; v1 = vd.y;
-        ok = 1;
-      }
-    }
-  };
-  if (np > 0) load_meta(0);
-  setup_queries();
+  // ---- walk the pages: metadata 64 pages at a time, chunks pipelined ----
   for (int base = 0; base < np; base += 64) {
     const int nb = np - base < 64 ? np - base : 64;
     if (base > 0) load_meta(base);
-    auto meta_of = [&](int i) -> PageMeta {
-      PageMeta m{};
-      const uint32_t kw0 = __builtin_amdgcn_readlane(k0, i), kw1 = __builtin_amdgcn_readlane(k1, i);
-      const uint32_t vw0 = __builtin_amdgcn_readlane(v0, i), vw1 = __builtin_amdgcn_readlane(v1, i);
-      const int good = __builtin_amdgcn_readlane(ok, i);
-      dc_page_desc kd, vd;
-      kd.block = kw0; kd.tokens = uint16_t(kw1 & 0xffff); kd.format = uint8_t(kw1 >> 16); kd.bits = uint8_t(kw1 >> 24);
-      vd.block = vw0; vd.tokens = uint16_t(vw1 & 0xffff); vd.format = uint8_t(vw1 >> 16); vd.bits = uint8_t(vw1 >> 24);
-      const BlobLayout KL = blob_layout(kd.format, kd.bits, kgeo), VL = blob_layout(vd.format, vd.bits, vgeo);
-      int T = kd.tokens < vd.tokens ? kd.tokens : vd.tokens;
-      if (T > CAP) T = CAP;
-      if (!good || (int64_t(kd.block) << 8) + KL.total > a.kpool.arena_bytes ||
-          (int64_t(vd.block) << 8) + VL.total > a.vpool.arena_bytes)
-        T = 0;
-      m.T = T;
-      m.kp = blob_ptr(a.kpool.arena, kd);
-      m.vp = blob_ptr(a.vpool.arena, vd);
-      m.kfmt = kd.format;
-      m.vfmt = vd.format;
-      m.vbits = vd.bits;
-      const bool km0 = is_m0(kd.format), vm0 = is_m0(vd.format);
-      m.ksc = km0 ? uint32_t(KL.scales_off) : 0u;
-      m.kbs = kd.format == DC_FMT_M0_AFFINE ? uint32_t(KL.bias_off) : m.ksc;
-      m.vsc = vm0 ? uint32_t(VL.scales_off) : 0u;
-      m.vbs = vd.format == DC_FMT_M0_AFFINE ? uint32_t(VL.bias_off) : m.vsc;
+    // lane i: everything about page base + i, once for the batch (vector
+    // work instead of per-page scalar work): blob addresses, token count,
+    // formats, scale / bias offsets, and its first chunk index in the batch
+    const BlobLayout KL = blob_layout(int(k1 >> 16) & 0xff, int(k1 >> 24), kgeo);
+    const BlobLayout VL = blob_layout(int(v1 >> 16) & 0xff, int(v1 >> 24), vgeo);
+    int T = min(int(k1 & 0xffff), int(v1 & 0xffff));
+    T = min(T, CAP);
+    if (!ok || lane >= nb || (int64_t(k0) << 8) + KL.total > a.kpool.arena_bytes ||
+        (int64_t(v0) << 8) + VL.total > a.vpool.arena_bytes)
+      T = 0;
+    const int kf = int(k1 >> 16) & 0xff, vf = int(v1 >> 16) & 0xff;
+    const uint32_t info = uint32_t(T) | (uint32_t(kf) << 16) | (uint32_t(vf) << 24);
+    const uint32_t ksc = is_m0(kf) ? uint32_t(KL.scales_off) : 0u;
+    const uint32_t kbs = kf == DC_FMT_M0_AFFINE ? uint32_t(KL.bias_off) : ksc;
+    const uint32_t vsc = is_m0(vf) ? uint32_t(VL.scales_off) : 0u;
+    const uint32_t vbs = vf == DC_FMT_M0_AFFINE ? uint32_t(VL.bias_off) : vsc;
+    const uint32_t koffs = ksc | (kbs << 16), voffs = vsc | (vbs << 16);  // offsets < 64 KiB for M0 pages
+    const uint32_t ktot = uint32_t(KL.total), vtot = uint32_t(VL.total);
+    const int nch = (T + 31) >> 5;
+    int cend = nch;  // inclusive prefix sum over the lanes: end chunk of page lane
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(cend, d, 64);
+      if (lane >= d) cend += v;
+    }
+    const int total = __builtin_amdgcn_readlane(cend, 63);
+    if (total == 0) continue;
+    // chunk j lies in the first page whose end chunk exceeds j
+    auto chunk_meta = [&](int j) -> PageMeta {
+      const int i = __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
+      PageMeta m;
+      // blob pointers stay derived from the arena arguments (global memory)
+      m.kp = reinterpret_cast<const uint8_t*>(a.kpool.arena) + (uint64_t(__builtin_amdgcn_readlane(k0, i)) << 8);
+      m.vp = reinterpret_cast<const uint8_t*>(a.vpool.arena) + (uint64_t(__builtin_amdgcn_readlane(v0, i)) << 8);
+      m.krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.kp), 0, int(__builtin_amdgcn_readlane(ktot, i)), 0x00020000);
+      m.vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0, int(__builtin_amdgcn_readlane(vtot, i)), 0x00020000);
+      const uint32_t inf = __builtin_amdgcn_readlane(info, i);
+      m.T = int(inf & 0xffff);
+      m.kfmt = int(inf >> 16) & 0xff;
+      m.vfmt = int(inf >> 24);
+      const uint32_t ko = __builtin_amdgcn_readlane(koffs, i), vo = __builtin_amdgcn_readlane(voffs, i);
+      m.ksc = ko & 0xffff;
+      m.kbs = ko >> 16;
+      m.vsc = vo & 0xffff;
+      m.vbs = vo >> 16;
+      m.c0 = (j - (__builtin_amdgcn_readlane(cend, i) - ((m.T + 31) >> 5))) * 32;
       return m;
     };
 
-    int i = 0;
-    PageMeta cur = meta_of(0);
-    while (cur.T <= 0 && i + 1 < nb) cur = meta_of(++i);
-    if (cur.T <= 0) continue;
-    int c0 = 0;
-    Regs R;
-    load_keys(cur, c0, R);
-    load_values(cur, c0, R);
-    while (true) {
-      // next chunk of this batch; the current chunk again when there is none
-      int ni = i, nc0 = c0 + 32;
-      PageMeta nm = cur;
-      if (nc0 >= cur.T) {
-        nc0 = 0;
-        ni = i + 1;
-        while (ni < nb) {
-          nm = meta_of(ni);
-          if (nm.T > 0) break;
-          ++ni;
-        }
+    if constexpr (HD <= 128) {
+      // two register sets in turn: the next chunk's loads fly into one while
+      // the chunk in the other is scored and mixed; after the last chunk the
+      // loads re-read that chunk (bytes just fetched)
+      Regs RA, RB;
+      int j = 0;
+      PageMeta cur = chunk_meta(0);
+      load_keys(cur, cur.c0, RA);
+      load_values(cur, cur.c0, RA);
+      auto step = [&](Regs& Rc, Regs& Rn) -> bool {
+        const bool more = j + 1 < total;
+        const PageMeta nm = more ? chunk_meta(j + 1) : cur;
+        load_keys(nm, nm.c0, Rn);
+        load_values(nm, nm.c0, Rn);
+        stage_chunk(Rc);
+        float Ls[8];
+        score_chunk(cur, Rc, Ls);
+        mix_chunk(cur, cur.c0, Ls);
+        cur = nm;
+        ++j;
+        return more;
+      };
+      while (step(RA, RB) && step(RB, RA)) {
       }
-      const bool more = ni < nb;
-      if (!more) {
-        nm = cur;
-        nc0 = c0;
-      }
-      float Ls[8];
-      if constexpr (HD <= 128) {
-        Regs Rn;  // the next chunk's loads fly while this one is scored and mixed
-        load_keys(nm, nc0, Rn);
-        load_values(nm, nc0, Rn);
-        stage_chunk(R);  // value codes and scales -> LDS
-        score_chunk(cur, R, Ls);
-        mix_chunk(cur, c0, Ls);
-        R = Rn;
-      } else {  // one register set: reload it as soon as the chunk has consumed it
+    } else {  // one register set: reload it as soon as the chunk has consumed it
+      Regs R;
+      PageMeta cur = chunk_meta(0);
+      load_keys(cur, cur.c0, R);
+      load_values(cur, cur.c0, R);
+      for (int j = 0; j < total; ++j) {
+        const bool more = j + 1 < total;
+        const PageMeta nm = more ? chunk_meta(j + 1) : cur;
+        float Ls[8];
         stage_chunk(R);
         score_chunk(cur, R, Ls);
-        load_keys(nm, nc0, R);
-        load_values(nm, nc0, R);
-        mix_chunk(cur, c0, Ls);
+        load_keys(nm, nm.c0, R);
+        load_values(nm, nm.c0, R);
+        mix_chunk(cur, cur.c0, Ls);
+        cur = nm;
       }
-      if (!more) break;
-      cur = nm;
-      i = ni;
-      c0 = nc0;
     }
   }
 
-  // ---- per wave: rows q and q + n_q, bias sums -> o[q][d]; then (m, l) ----
-  float l_tot = l_part;
-  l_tot += __shfl_xor(l_tot, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  // ---- end of the item: (m, l, o) of every head straight from the registers ----
+  float l = l_part;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);  // head r
+  if (any_affine) {
 #pragma unroll
-  for (int g = 0; g < VG; ++g) {
-    bsum[g] += __shfl_xor(bsum[g], 16, 64);
-    bsum[g] += __shfl_xor(bsum[g], 32, 64);
+    for (int g = 0; g < VG; ++g) {
+      bsum[g] += __shfl_xor(bsum[g], 16, 64);
+      bsum[g] += __shfl_xor(bsum[g], 32, 64);
+    }
   }
-  float* rows = reinterpret_cast<float*>(lds);  // [16][HD] D rows, then [16][VG] bias sums
+  const bool final_out = it.partial < 0;
+  if (!final_out && it.partial >= a.max_partials) return;
+  float* dst = final_out ? a.out + qbase : a.part_o + int64_t(it.partial) * nq * HD;
+  // D row 4 kb + i is head q = 4 kb + i, whose sum and bias sums live in lane q
+  float inv[4], bq[4][VG];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lq = __shfl(l, 4 * kb + i, 64);
+    inv[i] = final_out ? 1.f / fmaxf(lq, 1e-30f) : 1.f;
+#pragma unroll
+    for (int g = 0; g < VG; ++g) bq[i][g] = any_affine ? __shfl(bsum[g], 4 * kb + i, 64) : 0.f;
+  }
 #pragma unroll
   for (int g = 0; g < VG; ++g)
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       const int d = VGS * g + dcol + LPW4 * h;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rows[(4 * kb + i) * HD + d] = acc[g * H + h][i];
-    }
-  if (kb == 0 && r < nq)
-#pragma unroll
-    for (int g = 0; g < VG; ++g) rows[16 * HD + r * VG + g] = bsum[g];
-  constexpr int NO = 8 * HD / 64;  // o values per lane (n_q <= 8)
-  float o[NO];
-#pragma unroll
-  for (int k = 0; k < NO; ++k) {
-    const int idx = lane + 64 * k;
-    const int q = idx / HD, d = idx - q * HD;
-    o[k] = q < nq ? rows[q * HD + d] + rows[(q + nq) * HD + d] + rows[16 * HD + q * VG + d / VGS] : 0.f;
-  }
-#pragma unroll
-  for (int k = 0; k < NO; ++k) rows[lane + 64 * k] = o[k];  // o [8][HD]
-  if (kb == 0 && r < nq) {
-    rows[8 * HD + 2 * r] = m_run;
-    rows[8 * HD + 2 * r + 1] = l_tot;
-  }
-  __syncthreads();
-
-  // ---- workgroup: merge the waves' (m, l, o) by log-sum-exp ----
-  const bool final_out = it.partial < 0;
-  if (!final_out && it.partial >= a.max_partials) return;
-  float* dst = final_out ? a.out + qbase : a.part_o + int64_t(it.partial) * nq * HD;
-  for (int idx = threadIdx.x; idx < nq * HD; idx += kWaves * 64) {
-    const int q = idx / HD;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, reinterpret_cast<const float*>(lds_all + w * Cfg::WAVE_WORDS)[8 * HD + 2 * q]);
-    float L = 0.f, Ov = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float* wr = reinterpret_cast<const float*>(lds_all + w * Cfg::WAVE_WORDS);
-      const float mw = wr[8 * HD + 2 * q];
-      const float wt = mw == -INFINITY ? 0.f : exp2f(mw - M);
-      L += wr[8 * HD + 2 * q + 1] * wt;
-      Ov += wr[idx] * wt;
-    }
-    if (final_out) {
-      dst[idx] = L > 0.f ? Ov / L : 0.f;
-    } else {
-      dst[idx] = Ov;
-      if (idx - q * HD == 0) {
-        a.part_ml[(int64_t(it.partial) * nq + q) * 2 + 0] = M;
-        a.part_ml[(int64_t(it.partial) * nq + q) * 2 + 1] = L;
+      for (int i = 0; i < 4; ++i) {
+        const int q = 4 * kb + i;
+        if (q < nq) dst[q * HD + d] = (acc[g * H + h][i] + bq[i][g]) * inv[i];
       }
     }
+  if (!final_out && kb == 0 && head_live) {
+    a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 0] = m_ref;
+    a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 1] = l;
   }
 }
 
 template <int HD, int VGS, int KMODE, int VBITS, bool VM3>
 static int launch_t(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, VBITS, VM3>), dim3(uint32_t(a.n_items)), dim3(kWaves * 64),
-                     0, stream, a);
+  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, VBITS, VM3>), dim3(uint32_t(a.n_items)), dim3(64), 0, stream,
+                     a);
   return check_hip(hipGetLastError(), "decode_mfma_kernel launch");
 }
 
@@ -676,7 +695,7 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   *launched = false;
   const dc_page_geometry& kg = a.kpool.geometry;
   const dc_page_geometry& vg = a.vpool.geometry;
-  if (a.n_q > 8 || kg.layout != 0 || vg.layout != 0 || kg.group_size != 32) return DC_OK;
+  if (a.n_q > 16 || kg.layout != 0 || vg.layout != 0 || kg.group_size != 32) return DC_OK;
   if (kg.page_capacity % 32 != 0) return DC_OK;
   // formats present in the pools (bit = format * 9 + bits, as in dc_pool)
   const uint64_t km = a.kpool.format_mask, vm = a.vpool.format_mask;
@@ -702,6 +721,7 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   DC_EXACT(128, 64, KEYS_MIXED, 8, false)
   DC_EXACT(128, 64, KEYS_M0, 8, false)
   DC_EXACT(256, 32, KEYS_M0, 4, false)
+  DC_EXACT(256, 32, KEYS_M0, 4, true)
   DC_GENERAL(64, 32, 4)
   DC_GENERAL(64, 32, 8)
   DC_GENERAL(64, 64, 4)

@@ -20,12 +20,13 @@ import numpy as np
 from . import _lib
 from .page_pool import DevicePagePool, current_stream_ptr, dtype_code
 
-# Split long page lists so a launch has about one workgroup (of four
-# wavefronts) per CU for the 256 CUs: every wavefront then walks several pages,
-# which amortises its fixed cost (query set-up, the first loads, the final
-# combine) and keeps the split-K partials a small fraction of the bytes read.
-DEFAULT_TARGET_ITEMS = 256
-MIN_PAGES_PER_SPLIT = 4
+# A work item is one wavefront's share.  Split long page lists so a launch has
+# about one item per SIMD (256 CUs x 4): every wavefront then streams several
+# pages, which amortises its fixed cost (the page-table and descriptor reads
+# before the first load, the query set-up, the final write) and keeps the
+# split-K partials a small fraction of the bytes read.
+DEFAULT_TARGET_ITEMS = 1024
+MIN_PAGES_PER_SPLIT = 2
 
 
 def _torch():
