@@ -10,6 +10,10 @@
 // or 64, affine or symmetric) or M3 fp16; up to 16 query heads per KV head.
 // Other formats take the generic kernel (dc_decode.hip).
 //
+// Pipeline (head_dim <= 128): while chunk j is mixed, chunk j + 1 is staged
+// and scored and chunk j + 2 is being loaded, so the score's MFMA chain, the
+// mix's unpacking and the loads of one wavefront overlap.
+//
 // Exactness.  Every MFMA operand is exact: escape rows are fp16 already,
 // codes minus zero point are small integers, and each fp32 operand (scaled
 // query, softmax weight x value scale) is carried as two fp16 operands, its
@@ -52,14 +56,6 @@ __device__ __forceinline__ f32x4 mfma(const Frag& a, const Frag& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, b.h, c, 0, 0, 0);
 }
 
-// Page bytes are read once per launch: nontemporal loads stream them past
-// the caches, which measures about 12 % more HBM read bandwidth on gfx950
-// than ordinary loads for the same access pattern.
-template <typename T>
-__device__ __forceinline__ T stream_load(const T* p) {
-  return __builtin_nontemporal_load(p);
-}
-
 __device__ __forceinline__ uint32_t bits_of(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 h2_of(uint32_t v) { return __builtin_bit_cast(h2, v); }
 
@@ -68,13 +64,11 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) { return bits_of
 
 // Two fp32 values as their fp16 high parts rtz(x) and fp16 residuals
 // rtz(x - rtz(x)); x - rtz(x) is exact in fp32, so the pair carries x to
-// about 2^-22 relative.
+// about 2^-22 relative.  neg1 is -1 held in a register the compiler cannot
+// see through, so x - hi stays one fma with an fp16 operand (v_fma_mix_f32).
 struct Split2 {
   uint32_t hi, res;
 };
-// neg1 is -1 held in a register the compiler cannot see through, so
-// x - hi stays one fma with an fp16 operand (v_fma_mix_f32) instead of a
-// conversion and a subtraction.
 __device__ __forceinline__ Split2 split2(float x0, float x1, float neg1) {
   const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
   const float r0 = __builtin_fmaf(neg1, float(hi[0]), x0), r1 = __builtin_fmaf(neg1, float(hi[1]), x1);
@@ -109,15 +103,14 @@ struct MfmaCfg {
   static constexpr int NVS = (VSW + 63) / 64;
   static constexpr int NKS = (KSW + 63) / 64;
   static constexpr int VPAY = 0, VSC = VG * GSTRIDE, VBS = VSC + VSW, KSC = VBS + VSW, KBS = KSC + KSW;
-  static constexpr int LDS_WORDS = KBS + KSW;
+  static constexpr int STAGE = KBS + KSW;  // words of one staged chunk
   static_assert(VG * 8 * W % 64 == 0, "value pieces must spread evenly over the wave");
   static_assert(W % 4 == 0, "value code rows are staged in 16-byte pieces");
 };
 
-// Registers one chunk needs from HBM.  The next chunk's loads are issued
-// into them while the current chunk is scored and mixed.  Every chunk issues
-// the same loads whatever its page formats, so the compiler never has to
-// drain the queue to merge register versions.
+// Registers one chunk needs from HBM.  Every chunk issues the same loads
+// whatever its page formats, so the compiler never has to drain the queue to
+// merge register versions.
 template <int HD, int VGS, int VBITS, int KMODE>
 struct ChunkRegs {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
@@ -133,20 +126,23 @@ struct ChunkRegs {
 // One chunk: the page it belongs to (wave-uniform, in SGPRs) and its first token.
 struct PageMeta {
   __amdgpu_buffer_rsrc_t krs, vrs;  // buffer resources of the key / value blobs
-  const uint8_t* kp;
-  const uint8_t* vp;
-  int T;  // tokens of the page
+  const uint8_t* vp;                // value blob (M3 value rows are gathered through it)
+  int T;                            // tokens of the page
   int kfmt, vfmt;
   uint32_t ksc, kbs, vsc, vbs;  // byte offsets of scales / biases in the blobs (0 where absent)
   int c0;                       // first token of the chunk
 };
 
-template <int HD, int VGS, int KMODE, int VBITS, bool VM3>
-__global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(DecodeArgs a) {
+// KAFF / VAFF: the key / value pool may hold affine M0 pages (bias terms);
+// false drops that code entirely.
+template <int HD, int VGS, int KMODE, int VBITS, bool VM3, bool KAFF, bool VAFF>
+__global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
   using Regs = ChunkRegs<HD, VGS, VBITS, KMODE>;
   constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W, NACC = Cfg::NACC;
-  __shared__ uint32_t lds[Cfg::LDS_WORDS];
+  // two staged chunks in flight where the registers allow it
+  constexpr bool kPipe = HD <= 128 && !(VM3 && KMODE == KEYS_MIXED);
+  __shared__ uint32_t lds_all[(kPipe ? 2 : 1) * Cfg::STAGE];
 
   const dc_work_item it = a.items[blockIdx.x];
   const int lane = threadIdx.x;
@@ -254,7 +250,6 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
 #pragma unroll
   for (int g = 0; g < VG; ++g) bsum[g] = 0.f;
   float m_ref = -INFINITY, l_part = 0.f;
-  bool any_affine = false;
   float neg1 = -1.f;
   asm volatile("" : "+v"(neg1));
 
@@ -264,10 +259,6 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
     if constexpr (KMODE == KEYS_M3) return true;
     if constexpr (KMODE == KEYS_M0) return false;
     return m.kfmt == DC_FMT_M3_F16;
-  };
-  auto value_is_m0 = [&](const PageMeta& m) -> bool {
-    if constexpr (!VM3) return true;
-    return is_m0(m.vfmt);
   };
 
   // ---- loads of one chunk into registers ----
@@ -290,8 +281,9 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
     voff[k] = uint32_t(g * CAP * W * 4 + piece * 16);
   }
   const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
-  constexpr int kNT = 2;  // cache policy: nontemporal
-  auto load_keys = [&](const PageMeta& m, int c0, Regs& R) {
+  constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
+  auto load_chunk = [&](const PageMeta& m, Regs& R) {
+    const int c0 = m.c0;
     if constexpr (Regs::kWordKeys) {
 #pragma unroll
       for (int g = 0; g < KG; ++g)
@@ -315,22 +307,23 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
         R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), int(m.ksc) + c0 * KG * 2 + 256 * k, kNT);
-        R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), int(m.kbs) + c0 * KG * 2 + 256 * k, kNT);
+        if constexpr (KAFF)
+          R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), int(m.kbs) + c0 * KG * 2 + 256 * k, kNT);
       }
     }
-  };
-  auto load_values = [&](const PageMeta& m, int c0, Regs& R) {
 #pragma unroll
-    for (int k = 0; k < Cfg::NVP; ++k) R.vr[k] = __builtin_amdgcn_raw_buffer_load_b128(m.vrs, int(voff[k]), c0 * W * 4, kNT);
+    for (int k = 0; k < Cfg::NVP; ++k)
+      R.vr[k] = __builtin_amdgcn_raw_buffer_load_b128(m.vrs, int(voff[k]), c0 * W * 4, kNT);
 #pragma unroll
     for (int k = 0; k < Cfg::NVS; ++k) {
       R.vs[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), int(m.vsc) + c0 * VG * 2 + 256 * k, kNT);
-      R.vb[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), int(m.vbs) + c0 * VG * 2 + 256 * k, kNT);
+      if constexpr (VAFF)
+        R.vb[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), int(m.vbs) + c0 * VG * 2 + 256 * k, kNT);
     }
   };
 
-  // ---- registers -> LDS: value codes in padded rows, scales as loaded ([32][G] fp16) ----
-  auto stage_chunk = [&](const Regs& R) {
+  // ---- registers -> an LDS stage buffer: value codes in padded rows, scales as loaded ([32][G] fp16) ----
+  auto stage_chunk = [&](const Regs& R, uint32_t* lds) {
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k) {
       const int e = lane + 64 * k;
@@ -343,7 +336,7 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
       const int e = lane + 64 * k;
       if (Cfg::VSW % 64 == 0 || e < Cfg::VSW) {
         lds[Cfg::VSC + e] = R.vs[k];
-        lds[Cfg::VBS + e] = R.vb[k];
+        if constexpr (VAFF) lds[Cfg::VBS + e] = R.vb[k];
       }
     }
     if constexpr (KMODE != KEYS_M3) {
@@ -352,14 +345,14 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
         const int e = lane + 64 * k;
         if (Cfg::KSW % 64 == 0 || e < Cfg::KSW) {
           lds[Cfg::KSC + e] = R.ks[k];
-          lds[Cfg::KBS + e] = R.kbw[k];
+          if constexpr (KAFF) lds[Cfg::KBS + e] = R.kbw[k];
         }
       }
     }
   };
 
   // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
-  auto score_chunk = [&](const PageMeta& m, const Regs& R, float* Ls) {
+  auto score_chunk = [&](const PageMeta& m, const Regs& R, const uint32_t* lds, float* Ls) {
     if (key_is_m3(m)) {
       if constexpr (!Regs::kWordKeys) {
 #pragma unroll
@@ -377,8 +370,11 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
         }
       }
     } else if constexpr (KMODE != KEYS_M3) {  // M0 4-bit, group 32: scale and bias per group in fp32
-      const bool k_affine = m.kfmt == DC_FMT_M0_AFFINE;
+      // affine: codes n, bias b; symmetric: codes n - 7, no bias (bf = 0
+      // zeroes the bias words, which then alias the scales)
+      const bool k_affine = KAFF && m.kfmt == DC_FMT_M0_AFFINE;
       const float zp = k_affine ? 0.f : 7.f;
+      const float bf = k_affine ? 1.f : 0.f;
       // (1024 + n_lo, 1024 + 16 n_hi) -> (n_lo - zp, n_hi - zp)
       const h2 kmul = {(_Float16)1.f, (_Float16)0.0625f};
       const h2 kadd = {(_Float16)(-1024.f - zp), (_Float16)(-64.f - zp)};
@@ -390,8 +386,10 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
         for (int k = 0; k < 2 * KG; k += 4) {
           const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KSC + (8 * kb + 4 * hh) * KG / 2 + k);
           sw[k] = s4.x; sw[k + 1] = s4.y; sw[k + 2] = s4.z; sw[k + 3] = s4.w;
-          const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KBS + (8 * kb + 4 * hh) * KG / 2 + k);
-          bw[k] = b4.x; bw[k + 1] = b4.y; bw[k + 2] = b4.z; bw[k + 3] = b4.w;
+          if constexpr (KAFF) {
+            const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KBS + (8 * kb + 4 * hh) * KG / 2 + k);
+            bw[k] = b4.x; bw[k + 1] = b4.y; bw[k + 2] = b4.z; bw[k + 3] = b4.w;
+          }
         }
         float Lh[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -418,7 +416,7 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
           for (int i = 0; i < 4; ++i) {
             const int e = i * KG + g;
             Lh[i] += float(h2_of(sw[e >> 1])[e & 1]) * d[i];
-            if (k_affine) Lh[i] += float(h2_of(bw[e >> 1])[e & 1]) * qsum[g];
+            if constexpr (KAFF) Lh[i] += bf * float(h2_of(bw[e >> 1])[e & 1]) * qsum[g];
           }
         }
 #pragma unroll
@@ -427,12 +425,12 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
     }
   };
 
-  // ---- online softmax update and mix of one staged chunk ----
-  auto mix_chunk = [&](const PageMeta& m, int c0, float* Ls) {
-    if (c0 + 32 > m.T) {
+  // ---- online softmax of one scored chunk: weights pa of head r on tokens 8 kb + e ----
+  auto softmax_chunk = [&](const PageMeta& m, float* Ls, float* pa) {
+    if (m.c0 + 32 > m.T) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (c0 + 8 * kb + e >= m.T) Ls[e] = -INFINITY;
+        if (m.c0 + 8 * kb + e >= m.T) Ls[e] = -INFINITY;
     }
     float mx = Ls[0];
 #pragma unroll
@@ -456,28 +454,36 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][i] *= arow[i];
     }
-    // weights of head r on tokens 8 kb + e (0 past the page end and for rows >= n_q)
-    float pa[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float w = __builtin_amdgcn_exp2f(Ls[e] - m_ref);
       pa[e] = head_live ? w : 0.f;
       l_part += pa[e];
     }
-    if (value_is_m0(m)) {
-      const bool v_affine = m.vfmt == DC_FMT_M0_AFFINE;
-      any_affine = any_affine || v_affine;
+  };
+
+  // ---- mix of one staged chunk with its weights ----
+  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa) {
+    bool v_m0 = true;
+    if constexpr (VM3) v_m0 = is_m0(m.vfmt);
+    if (v_m0) {
+      const bool v_affine = VAFF && m.vfmt == DC_FMT_M0_AFFINE;
       const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
+      const float bf = v_affine ? 1.f : 0.f;
       // codes become fp16 (1024 + c), or (1024 + 16 c) for a code in the high
       // nibble of its byte; one packed fma maps either to c - zp exactly
       const h2 vadd = VBITS == 4 && (jj & 1) ? h2{(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)}
                                               : h2{(_Float16)(-1024.f - zp), (_Float16)(-1024.f - zp)};
-      // scales of tokens 8 kb + e, all groups: [8][VG] fp16 = 4 VG words
-      uint32_t sw[4 * VG];
+      // scales (and biases) of tokens 8 kb + e, all groups: [8][VG] fp16 = 4 VG words
+      uint32_t sw[4 * VG], bw[4 * VG];
 #pragma unroll
       for (int k = 0; k < 4 * VG; k += 4) {
         const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VSC + 4 * VG * kb + k);
         sw[k] = s4.x; sw[k + 1] = s4.y; sw[k + 2] = s4.z; sw[k + 3] = s4.w;
+        if constexpr (VAFF) {
+          const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VBS + 4 * VG * kb + k);
+          bw[k] = b4.x; bw[k + 1] = b4.y; bw[k + 2] = b4.z; bw[k + 3] = b4.w;
+        }
       }
 #pragma unroll
       for (int g = 0; g < VG; ++g) {
@@ -491,15 +497,9 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
           const Split2 sp = split2(x0, x1, neg1);
           fa_hi.u[pp] = sp.hi;
           fa_res.u[pp] = sp.res;
-        }
-        if (v_affine) {
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const int e0 = (2 * pp) * VG + g, e1 = (2 * pp + 1) * VG + g;
-            const uint32_t b0 = lds[Cfg::VBS + 4 * VG * kb + (e0 >> 1)];
-            const uint32_t b1 = lds[Cfg::VBS + 4 * VG * kb + (e1 >> 1)];
-            bsum[g] += pa[2 * pp] * float(h2_of(b0)[e0 & 1]) + pa[2 * pp + 1] * float(h2_of(b1)[e1 & 1]);
-          }
+          if constexpr (VAFF)
+            bsum[g] += bf * (pa[2 * pp] * float(h2_of(bw[e0 >> 1])[e0 & 1]) +
+                             pa[2 * pp + 1] * float(h2_of(bw[e1 >> 1])[e1 & 1]));
         }
         const uint32_t* P = lds + Cfg::VPAY + g * Cfg::GSTRIDE + vrow;  // token 8 kb + e at P[e W]
 #pragma unroll
@@ -535,7 +535,7 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
           Frag fb;
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            const int t0 = c0 + 8 * kb + 2 * pp;
+            const int t0 = m.c0 + 8 * kb + 2 * pp;
             const uint32_t lo = t0 < m.T ? V[t0 * HD + d] : 0u;
             const uint32_t hi = t0 + 1 < m.T ? V[(t0 + 1) * HD + d] : 0u;
             fb.u[pp] = lo | (hi << 16);
@@ -551,8 +551,8 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
     const int nb = np - base < 64 ? np - base : 64;
     if (base > 0) load_meta(base);
     // lane i: everything about page base + i, once for the batch (vector
-    // work instead of per-page scalar work): blob addresses, token count,
-    // formats, scale / bias offsets, and its first chunk index in the batch
+    // work instead of per-page scalar work): token count, formats, blob
+    // sizes, scale / bias offsets, and its end chunk index in the batch
     const BlobLayout KL = blob_layout(int(k1 >> 16) & 0xff, int(k1 >> 24), kgeo);
     const BlobLayout VL = blob_layout(int(v1 >> 16) & 0xff, int(v1 >> 24), vgeo);
     int T = min(int(k1 & 0xffff), int(v1 & 0xffff));
@@ -568,12 +568,16 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
     const uint32_t vbs = vf == DC_FMT_M0_AFFINE ? uint32_t(VL.bias_off) : vsc;
     const uint32_t koffs = ksc | (kbs << 16), voffs = vsc | (vbs << 16);  // offsets < 64 KiB for M0 pages
     const uint32_t ktot = uint32_t(KL.total), vtot = uint32_t(VL.total);
-    const int nch = (T + 31) >> 5;
-    int cend = nch;  // inclusive prefix sum over the lanes: end chunk of page lane
+    const int nch = (T + 31) >> 5;  // < 16 (capacity <= 256)
+    // inclusive prefix sum over the lanes (end chunk of page lane), bit by
+    // bit: ballot of the bit, count of set lanes at or below this one
+    int cend = 0;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int v = __shfl_up(cend, d, 64);
-      if (lane >= d) cend += v;
+    for (int b = 0; b < 4; ++b) {
+      const int bit = (nch >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      const int below = __builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u));
+      cend += (below + bit) << b;
     }
     const int total = __builtin_amdgcn_readlane(cend, 63);
     if (total == 0) continue;
@@ -582,10 +586,13 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
       const int i = __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
       PageMeta m;
       // blob pointers stay derived from the arena arguments (global memory)
-      m.kp = reinterpret_cast<const uint8_t*>(a.kpool.arena) + (uint64_t(__builtin_amdgcn_readlane(k0, i)) << 8);
+      const uint8_t* kp =
+          reinterpret_cast<const uint8_t*>(a.kpool.arena) + (uint64_t(__builtin_amdgcn_readlane(k0, i)) << 8);
       m.vp = reinterpret_cast<const uint8_t*>(a.vpool.arena) + (uint64_t(__builtin_amdgcn_readlane(v0, i)) << 8);
-      m.krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.kp), 0, int(__builtin_amdgcn_readlane(ktot, i)), 0x00020000);
-      m.vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0, int(__builtin_amdgcn_readlane(vtot, i)), 0x00020000);
+      m.krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(kp), 0, int(__builtin_amdgcn_readlane(ktot, i)),
+                                                0x00020000);
+      m.vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0,
+                                                int(__builtin_amdgcn_readlane(vtot, i)), 0x00020000);
       const uint32_t inf = __builtin_amdgcn_readlane(info, i);
       m.T = int(inf & 0xffff);
       m.kfmt = int(inf >> 16) & 0xff;
@@ -599,44 +606,54 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
       return m;
     };
 
-    if constexpr (HD <= 128) {
-      // two register sets in turn: the next chunk's loads fly into one while
-      // the chunk in the other is scored and mixed; after the last chunk the
+    if constexpr (kPipe) {
+      // chunk j is mixed from stage buffer j % 2 while chunk j + 1 is staged
+      // into the other buffer and scored, and the loads of chunk j + 2 fly
+      // into the register set chunk j + 1 came in; after the last chunk the
       // loads re-read that chunk (bytes just fetched)
+      uint32_t* const buf0 = lds_all;
+      uint32_t* const buf1 = lds_all + Cfg::STAGE;
       Regs RA, RB;
-      int j = 0;
       PageMeta cur = chunk_meta(0);
-      load_keys(cur, cur.c0, RA);
-      load_values(cur, cur.c0, RA);
-      auto step = [&](Regs& Rc, Regs& Rn) -> bool {
-        const bool more = j + 1 < total;
-        const PageMeta nm = more ? chunk_meta(j + 1) : cur;
-        load_keys(nm, nm.c0, Rn);
-        load_values(nm, nm.c0, Rn);
-        stage_chunk(Rc);
-        float Ls[8];
-        score_chunk(cur, Rc, Ls);
-        mix_chunk(cur, cur.c0, Ls);
-        cur = nm;
+      PageMeta nxt = total > 1 ? chunk_meta(1) : cur;
+      load_chunk(cur, RA);
+      load_chunk(nxt, RB);
+      float Ls[8], pa[8];
+      stage_chunk(RA, buf0);
+      score_chunk(cur, RA, buf0, Ls);
+      softmax_chunk(cur, Ls, pa);
+      int j = 0;
+      auto step = [&](Regs& X, Regs& Y, uint32_t* bm, uint32_t* bs) -> bool {
+        if (j + 1 >= total) {  // last chunk: mix only
+          mix_chunk(cur, bm, pa);
+          return false;
+        }
+        const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : nxt;
+        load_chunk(n2, Y);
+        float Ln[8];
+        stage_chunk(X, bs);
+        score_chunk(nxt, X, bs, Ln);
+        mix_chunk(cur, bm, pa);
+        softmax_chunk(nxt, Ln, pa);
+        cur = nxt;
+        nxt = n2;
         ++j;
-        return more;
+        return true;
       };
-      while (step(RA, RB) && step(RB, RA)) {
+      while (step(RB, RA, buf0, buf1) && step(RA, RB, buf1, buf0)) {
       }
-    } else {  // one register set: reload it as soon as the chunk has consumed it
+    } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
       Regs R;
       PageMeta cur = chunk_meta(0);
-      load_keys(cur, cur.c0, R);
-      load_values(cur, cur.c0, R);
+      load_chunk(cur, R);
       for (int j = 0; j < total; ++j) {
-        const bool more = j + 1 < total;
-        const PageMeta nm = more ? chunk_meta(j + 1) : cur;
-        float Ls[8];
-        stage_chunk(R);
-        score_chunk(cur, R, Ls);
-        load_keys(nm, nm.c0, R);
-        load_values(nm, nm.c0, R);
-        mix_chunk(cur, cur.c0, Ls);
+        const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : cur;
+        float Ls[8], pa[8];
+        stage_chunk(R, lds_all);
+        score_chunk(cur, R, lds_all, Ls);
+        load_chunk(nm, R);
+        softmax_chunk(cur, Ls, pa);
+        mix_chunk(cur, lds_all, pa);
         cur = nm;
       }
     }
@@ -646,7 +663,7 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
   float l = l_part;
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);  // head r
-  if (any_affine) {
+  if constexpr (VAFF) {
 #pragma unroll
     for (int g = 0; g < VG; ++g) {
       bsum[g] += __shfl_xor(bsum[g], 16, 64);
@@ -663,29 +680,27 @@ __global__ void __launch_bounds__(64, HD >= 256 ? 1 : 2) decode_mfma_kernel(Deco
     const float lq = __shfl(l, 4 * kb + i, 64);
     inv[i] = final_out ? 1.f / fmaxf(lq, 1e-30f) : 1.f;
 #pragma unroll
-    for (int g = 0; g < VG; ++g) bq[i][g] = any_affine ? __shfl(bsum[g], 4 * kb + i, 64) : 0.f;
+    for (int g = 0; g < VG; ++g) bq[i][g] = VAFF ? __shfl(bsum[g], 4 * kb + i, 64) : 0.f;
   }
+  // one per-lane pointer (row 4 kb, column dcol); every store is a constant offset from it
+  float* dq = dst + 4 * kb * HD + dcol;
 #pragma unroll
-  for (int g = 0; g < VG; ++g)
+  for (int i = 0; i < 4; ++i)
+    if (4 * kb + i < nq)
 #pragma unroll
-    for (int h = 0; h < H; ++h) {
-      const int d = VGS * g + dcol + LPW4 * h;
+      for (int g = 0; g < VG; ++g)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = 4 * kb + i;
-        if (q < nq) dst[q * HD + d] = (acc[g * H + h][i] + bq[i][g]) * inv[i];
-      }
-    }
+        for (int h = 0; h < H; ++h) dq[i * HD + VGS * g + LPW4 * h] = (acc[g * H + h][i] + bq[i][g]) * inv[i];
   if (!final_out && kb == 0 && head_live) {
     a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 0] = m_ref;
     a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 1] = l;
   }
 }
 
-template <int HD, int VGS, int KMODE, int VBITS, bool VM3>
+template <int HD, int VGS, int KMODE, int VBITS, bool VM3, bool KAFF, bool VAFF>
 static int launch_t(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, VBITS, VM3>), dim3(uint32_t(a.n_items)), dim3(64), 0, stream,
-                     a);
+  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, VBITS, VM3, KAFF, VAFF>), dim3(uint32_t(a.n_items)),
+                     dim3(64), 0, stream, a);
   return check_hip(hipGetLastError(), "decode_mfma_kernel launch");
 }
 
@@ -702,26 +717,32 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   const uint64_t k_m3 = fbit(DC_FMT_M3_F16, 0), k_m0 = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
   const uint64_t v4 = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
   const uint64_t v8 = fbit(DC_FMT_M0_AFFINE, 8) | fbit(DC_FMT_M0_SYMMETRIC, 8);
+  const uint64_t aff = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_AFFINE, 8);
   if (km == 0 || vm == 0 || (km & ~(k_m3 | k_m0)) || (vm & ~(k_m3 | v4 | v8))) return DC_OK;
   if ((vm & v4) && (vm & v8)) return DC_OK;  // one value code width per launch
   const int kmode = (km & k_m3) && (km & k_m0) ? KEYS_MIXED : (km & k_m3) ? KEYS_M3 : KEYS_M0;
   const int vbits = (vm & v8) ? 8 : 4;
   const bool vm3 = (vm & k_m3) != 0;
+  const bool kaff = (km & aff) != 0, vaff = (vm & aff) != 0;
   const int hd = kg.head_dim, vgs = vg.group_size;
   int rc = -1;
-  // specialised instantiations for common pools, a general one per shape otherwise
-#define DC_EXACT(HD_, VGS_, KM_, VB_, VM3_)                                                          \
-  if (rc < 0 && hd == HD_ && vgs == VGS_ && kmode == KM_ && vbits == VB_ && vm3 == VM3_) \
-    rc = launch_t<HD_, VGS_, KM_, VB_, VM3_>(a, stream);
-#define DC_GENERAL(HD_, VGS_, VB_) \
-  if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_) rc = launch_t<HD_, VGS_, KEYS_MIXED, VB_, true>(a, stream);
-  DC_EXACT(64, 32, KEYS_M0, 4, false)
-  DC_EXACT(128, 32, KEYS_M3, 4, false)
-  DC_EXACT(128, 32, KEYS_M0, 4, false)
-  DC_EXACT(128, 64, KEYS_MIXED, 8, false)
-  DC_EXACT(128, 64, KEYS_M0, 8, false)
-  DC_EXACT(256, 32, KEYS_M0, 4, false)
-  DC_EXACT(256, 32, KEYS_M0, 4, true)
+  // specialised instantiations for the common pools (every BASELINE
+  // configuration), a general one per shape otherwise
+#define DC_EXACT(HD_, VGS_, KM_, VB_, VM3_, KA_, VA_)                                                    \
+  if (rc < 0 && hd == HD_ && vgs == VGS_ && kmode == KM_ && vbits == VB_ && vm3 == VM3_ && kaff == KA_ && \
+      vaff == VA_)                                                                                       \
+    rc = launch_t<HD_, VGS_, KM_, VB_, VM3_, KA_, VA_>(a, stream);
+#define DC_GENERAL(HD_, VGS_, VB_)                        \
+  if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_) \
+    rc = launch_t<HD_, VGS_, KEYS_MIXED, VB_, true, true, true>(a, stream);
+  DC_EXACT(64, 32, KEYS_M0, 4, false, false, false)     // config 1
+  DC_EXACT(64, 32, KEYS_M0, 4, false, true, true)       // config 2
+  DC_EXACT(128, 32, KEYS_M3, 4, false, false, false)    // config 3
+  DC_EXACT(128, 64, KEYS_MIXED, 8, false, true, false)  // config 4
+  DC_EXACT(128, 64, KEYS_M0, 8, false, true, false)
+  DC_EXACT(128, 32, KEYS_M0, 4, false, true, true)
+  DC_EXACT(256, 32, KEYS_MIXED, 4, true, true, true)  // config 5 (fp16 recent window)
+  DC_EXACT(256, 32, KEYS_M0, 4, false, true, true)
   DC_GENERAL(64, 32, 4)
   DC_GENERAL(64, 32, 8)
   DC_GENERAL(64, 64, 4)
