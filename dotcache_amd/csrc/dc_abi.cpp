@@ -84,11 +84,13 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
       const int32_t first_partial = np;
       for (int32_t s = 0; s < splits; ++s) {
         if (items && ni < max_items) {
+          // near-equal splits (sizes differ by at most one page), so no item
+          // is a short remainder and none exceeds pages_per_split
           dc_work_item& it = items[ni];
           it.seq = b;
           it.kv_head = h;
-          it.page_begin = s * per;
-          it.page_end = s * per + per < pages ? s * per + per : pages;
+          it.page_begin = int32_t(int64_t(s) * pages / splits);
+          it.page_end = int32_t(int64_t(s + 1) * pages / splits);
           it.partial = splits > 1 ? np : -1;
           it.reserved[0] = it.reserved[1] = it.reserved[2] = 0;
         }

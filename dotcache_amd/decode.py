@@ -49,11 +49,40 @@ class DecodePlan:
 _plan_cache: dict = {}
 
 
-def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items: int = DEFAULT_TARGET_ITEMS) -> int:
-    """Pages per work item so that the launch has about ``target_items`` items."""
-    total = int(np.sum(seq_pages)) * n_kv_heads
-    per = max(MIN_PAGES_PER_SPLIT, -(-total // max(target_items, 1)))
-    return int(min(per, max(int(np.max(seq_pages)), 1)))
+def default_target_items() -> int:
+    """Work items one launch should have: one per SIMD of the current device
+    (4 per CU), so a one-wavefront-per-SIMD kernel runs every item in a single
+    round."""
+    try:
+        torch = _torch()
+        if torch.cuda.is_available():
+            return 4 * int(torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count)
+    except Exception:
+        pass
+    return DEFAULT_TARGET_ITEMS
+
+
+def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items: int | None = None) -> int:
+    """Smallest pages-per-split (at least MIN_PAGES_PER_SPLIT) for which the
+    plan has at most ``target_items`` items; the planner then cuts every
+    sequence into near-equal items of at most that many pages."""
+    sp = np.asarray(seq_pages, dtype=np.int64)
+    target = int(target_items) if target_items else default_target_items()
+    top = max(int(sp.max()), 1)
+
+    def n_items(per: int) -> int:
+        return int(n_kv_heads * np.sum(-(-sp // per)))
+
+    lo, hi = min(MIN_PAGES_PER_SPLIT, top), top
+    if n_items(hi) > target:
+        return hi  # more sequences x heads than items: one item each
+    while lo < hi:
+        mid = (lo + hi) // 2
+        if n_items(mid) <= target:
+            hi = mid
+        else:
+            lo = mid + 1
+    return int(lo)
 
 
 def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *, device="cuda") -> DecodePlan:

@@ -180,9 +180,10 @@ int dc_softmax_rows(float* x /* device */, int32_t n_rows, int32_t n_cols, int64
 
 /* ---- read path: fused paged decode ------------------------------------ */
 
-/* Host-only planner: split each (sequence, kv_head)'s page list into work
- * items of at most pages_per_split pages (pages_per_split <= 0: one item
- * per sequence), and emit merge items for sequences that were split.
+/* Host-only planner: split each (sequence, kv_head)'s page list into
+ * ceil(pages / pages_per_split) work items of near-equal size (at most
+ * pages_per_split pages each; pages_per_split <= 0: one item per sequence),
+ * and emit merge items for sequences that were split.
  * seq_pages: host [n_seqs].  Returns DC_ESPACE if the output arrays are too
  * small (counts are still written). */
 int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t pages_per_split,
