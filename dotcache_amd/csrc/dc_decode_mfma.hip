@@ -582,6 +582,13 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     const int total = __builtin_amdgcn_readlane(cend, 63);
     if (total == 0) continue;
     // chunk j lies in the first page whose end chunk exceeds j
+    // a chunk past the end: the same loads against empty buffer resources,
+    // which return zeros without touching memory
+    auto no_chunk = [&](PageMeta m) -> PageMeta {
+      m.krs = __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0x00020000);
+      m.vrs = m.krs;
+      return m;
+    };
     auto chunk_meta = [&](int j) -> PageMeta {
       const int i = __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
       PageMeta m;
@@ -609,13 +616,13 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     if constexpr (kPipe) {
       // chunk j is mixed from stage buffer j % 2 while chunk j + 1 is staged
       // into the other buffer and scored, and the loads of chunk j + 2 fly
-      // into the register set chunk j + 1 came in; after the last chunk the
-      // loads re-read that chunk (bytes just fetched)
+      // into the register set chunk j + 1 came in; past the last chunk the
+      // loads go to an empty resource (no memory traffic)
       uint32_t* const buf0 = lds_all;
       uint32_t* const buf1 = lds_all + Cfg::STAGE;
       Regs RA, RB;
       PageMeta cur = chunk_meta(0);
-      PageMeta nxt = total > 1 ? chunk_meta(1) : cur;
+      PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
       load_chunk(cur, RA);
       load_chunk(nxt, RB);
       float Ls[8], pa[8];
@@ -628,7 +635,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           mix_chunk(cur, bm, pa);
           return false;
         }
-        const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : nxt;
+        const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : no_chunk(nxt);
         load_chunk(n2, Y);
         float Ln[8];
         stage_chunk(X, bs);
@@ -647,7 +654,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       PageMeta cur = chunk_meta(0);
       load_chunk(cur, R);
       for (int j = 0; j < total; ++j) {
-        const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : cur;
+        const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
         float Ls[8], pa[8];
         stage_chunk(R, lds_all);
         score_chunk(cur, R, lds_all, Ls);
