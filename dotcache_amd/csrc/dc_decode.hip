@@ -193,53 +193,97 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
   }
 }
 
-// One wavefront per (merge item, query head j): the lanes reduce the
-// partials' (m, l) to (M, L), then each lane combines four channels,
-// out = sum_s o_s exp2(m_s - M) / L (log2 domain), four partials in flight.
-__global__ void __launch_bounds__(64) merge_kernel(const dc_merge_item* __restrict__ merges, const float* part_o,
-                                                   const float* part_ml, float* out, int32_t n_kv_heads,
-                                                   int32_t nq, int32_t hd, int64_t max_partials) {
+// One 256-thread block per (merge item, query head j), viewed as rows of
+// C = head_dim / V threads, each thread holding V channels.  Row r combines
+// partials r, r + R, ... (R = 256 / C rows) against its own running maximum,
+// loading each partial's (m, l) and o together, so all of a merge's loads
+// are in flight at once; the rows' (m_r, l_r, o_r) are then combined through
+// LDS:  M = max m_r,  out = sum_r o_r exp2(m_r - M) / sum_r l_r exp2(m_r - M)
+// (log2 domain).
+template <int V>
+__global__ void __launch_bounds__(256) merge_kernel(const dc_merge_item* __restrict__ merges, const float* part_o,
+                                                    const float* part_ml, float* out, int32_t n_kv_heads,
+                                                    int32_t nq, int32_t hd, int64_t max_partials) {
+  struct Vec {
+    float v[V];
+  };
+  __shared__ Vec red[256];
+  __shared__ float2 red_ml[256];
   const dc_merge_item mi = merges[blockIdx.x];
-  const int j = blockIdx.y, lane = threadIdx.x;
+  const int j = blockIdx.y, t = threadIdx.x;
   if (mi.partial_begin < 0 || mi.count <= 0 || int64_t(mi.partial_begin) + mi.count > max_partials) return;
-  const float* ml = part_ml + (int64_t(mi.partial_begin) * nq + j) * 2;  // partial s at ml[2 nq s]
-  float M = -INFINITY;
-  for (int s = lane; s < mi.count; s += 64) M = fmaxf(M, ml[int64_t(s) * nq * 2]);
-  M = wave_max(M);
-  float L = 0.f;
-  for (int s = lane; s < mi.count; s += 64) {
-    const float m = ml[int64_t(s) * nq * 2];
-    L += m == -INFINITY ? 0.f : ml[int64_t(s) * nq * 2 + 1] * exp2f(m - M);
+  const int C = hd / V, R = 256 / C;  // hd <= 256, so R >= 1
+  const int row = t / C, col = t - row * C;
+  const float* ml = part_ml + (int64_t(mi.partial_begin) * nq + j) * 2;             // partial s at ml[2 nq s]
+  const float* po = part_o + (int64_t(mi.partial_begin) * nq + j) * hd + col * V;  // partial s at po[nq hd s]
+  const int64_t mstep = int64_t(nq) * 2, step = int64_t(nq) * hd;
+  float m_r = -INFINITY, l_r = 0.f;
+  Vec acc;
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc.v[e] = 0.f;
+  if (row < R) {
+    // four partials per pass; a slot past the count loads partial s0 again
+    // (always in bounds) and is masked off, so no load waits on a branch
+    for (int s0 = row; s0 < mi.count; s0 += 4 * R) {
+      float mv[4], lv[4];
+      Vec xv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = s0 + u * R < mi.count ? s0 + u * R : s0;
+        mv[u] = ml[s * mstep];
+        lv[u] = ml[s * mstep + 1];
+        if constexpr (V == 4) {
+          const float4 y = *reinterpret_cast<const float4*>(po + s * step);
+          xv[u].v[0] = y.x;
+          xv[u].v[1] = y.y;
+          xv[u].v[2] = y.z;
+          xv[u].v[3] = y.w;
+        } else {
+          xv[u].v[0] = po[s * step];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u * R >= mi.count) mv[u] = -INFINITY;
+      const float m_new = fmaxf(fmaxf(m_r, fmaxf(mv[0], mv[1])), fmaxf(mv[2], mv[3]));
+      if (m_new == -INFINITY) continue;  // every partial so far is empty
+      const float c_old = m_r == -INFINITY ? 0.f : exp2f(m_r - m_new);
+      l_r *= c_old;
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc.v[e] *= c_old;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float c = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - m_new);  // an empty partial adds nothing
+        l_r += lv[u] * c;
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc.v[e] += xv[u].v[e] * c;
+      }
+      m_r = m_new;
+    }
   }
-  const float inv = 1.f / fmaxf(wave_sum(L), 1e-30f);
-  const float* po = part_o + (int64_t(mi.partial_begin) * nq + j) * hd;  // partial s at po[nq hd s]
-  float* o = out + ((int64_t(mi.seq) * n_kv_heads + mi.kv_head) * nq + j) * hd;
-  const int64_t step = int64_t(nq) * hd;
-  if ((hd & 3) == 0 && ((reinterpret_cast<uintptr_t>(po) | reinterpret_cast<uintptr_t>(o) | uintptr_t(step * 4)) & 15) == 0) {
-    for (int c = 4 * lane; c < hd; c += 256) {
-      float4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int s = 0; s < mi.count; ++s) {
-        const float m = ml[int64_t(s) * nq * 2];
-        const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-        const float4 v = *reinterpret_cast<const float4*>(po + s * step + c);
-        acc.x += v.x * w;
-        acc.y += v.y * w;
-        acc.z += v.z * w;
-        acc.w += v.w * w;
+  red[t] = acc;
+  red_ml[t] = float2{m_r, l_r};
+  __syncthreads();
+  if (t < C) {
+    float M = -INFINITY;
+    for (int r = 0; r < R; ++r) M = fmaxf(M, red_ml[r * C + t].x);
+    float L = 0.f;
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc.v[e] = 0.f;
+    if (M != -INFINITY)
+      for (int r = 0; r < R; ++r) {
+        const float2 q = red_ml[r * C + t];
+        const float w = q.x == -INFINITY ? 0.f : exp2f(q.x - M);
+        L += q.y * w;
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc.v[e] += red[r * C + t].v[e] * w;
       }
-      *reinterpret_cast<float4*>(o + c) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
-    }
-  } else {
-    for (int c = lane; c < hd; c += 64) {
-      float acc = 0.f;
-#pragma unroll 4
-      for (int s = 0; s < mi.count; ++s) {
-        const float m = ml[int64_t(s) * nq * 2];
-        acc += m == -INFINITY ? 0.f : po[s * step + c] * exp2f(m - M);
-      }
-      o[c] = acc * inv;
-    }
+    const float inv = 1.f / fmaxf(L, 1e-30f);
+    float* o = out + ((int64_t(mi.seq) * n_kv_heads + mi.kv_head) * nq + j) * hd + t * V;
+    if constexpr (V == 4)
+      *reinterpret_cast<float4*>(o) = float4{acc.v[0] * inv, acc.v[1] * inv, acc.v[2] * inv, acc.v[3] * inv};
+    else
+      o[0] = acc.v[0] * inv;
   }
 }
 
@@ -259,8 +303,16 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream) {
 
 int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream) {
   if (n_merges <= 0) return DC_OK;
-  hipLaunchKernelGGL(merge_kernel, dim3(uint32_t(n_merges), uint32_t(a.n_q)), dim3(64), 0, stream, merges,
-                     a.part_o, a.part_ml, a.out, a.n_kv_heads, a.n_q, a.kpool.geometry.head_dim, a.max_partials);
+  const int hd = a.kpool.geometry.head_dim;
+  // float4 rows when every partial row and output row starts 16-byte aligned
+  const bool vec4 = (hd & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.part_o) | reinterpret_cast<uintptr_t>(a.out)) & 15) == 0;
+  const dim3 grid(uint32_t(n_merges), uint32_t(a.n_q));
+  if (vec4)
+    hipLaunchKernelGGL(merge_kernel<4>, grid, dim3(256), 0, stream, merges, a.part_o, a.part_ml, a.out, a.n_kv_heads,
+                       a.n_q, hd, a.max_partials);
+  else
+    hipLaunchKernelGGL(merge_kernel<1>, grid, dim3(256), 0, stream, merges, a.part_o, a.part_ml, a.out, a.n_kv_heads,
+                       a.n_q, hd, a.max_partials);
   return check_hip(hipGetLastError(), "merge_kernel launch");
 }
 

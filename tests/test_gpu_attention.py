@@ -199,3 +199,47 @@ def test_fused_decode_peaked_attention_and_small_values():
     want = O.decode_grouped(q, [kp], [vp])
     got = fused(list(q), [[to_product_page(p) for p in kp]], [[to_product_page(p) for p in vp]]).cpu().numpy()
     assert np.max(np.abs(got - want)) < 1e-3
+
+
+@pytest.mark.parametrize("hd", [128, 30])
+def test_lse_merge_matches_float64(hd):
+    """dc_lse_merge on hand-made partials (m, l, o), log2 domain: ragged
+    counts, empty partials (m = -inf) and a merge whose partials are all
+    empty.  head_dim 30 takes the one-channel-per-thread path."""
+    import ctypes as C
+
+    import torch
+
+    from dotcache_amd import _lib
+    from dotcache_amd.page_pool import current_stream_ptr
+
+    rng = np.random.default_rng(hd)
+    B, H, Q = 2, 2, 3
+    counts = [5, 1, 40, 3]                  # (seq, kv_head) in row-major order
+    n_part = sum(counts) + 2                # two unused slots at the end
+    part_o = rng.normal(size=(n_part, Q, hd)).astype(np.float32)
+    m = (rng.normal(size=(n_part, Q)) * 8).astype(np.float32)
+    l = rng.uniform(0.5, 40.0, size=(n_part, Q)).astype(np.float32)
+    m[2, 1] = -np.inf                       # an empty partial inside merge 0
+    l[2, 1] = 0.0
+    begins = np.cumsum([0] + counts[:-1])
+    m[begins[3]:begins[3] + 3] = -np.inf    # merge 3: every partial empty
+    l[begins[3]:begins[3] + 3] = 0.0
+    ml = np.stack([m, l], axis=-1)
+    ws = torch.from_numpy(np.concatenate([part_o.ravel(), ml.ravel()]).astype(np.float32)).cuda()
+    items = np.array([[i // H, i % H, begins[i], counts[i]] for i in range(len(counts))], np.int32)
+    merges = torch.from_numpy(items.ravel().view(np.uint8).copy()).cuda()
+    out = torch.full((B, H, Q, hd), 7.0, dtype=torch.float32, device="cuda")
+    st = _lib.lib().dc_lse_merge(C.c_void_p(merges.data_ptr()), len(counts), C.c_void_p(ws.data_ptr()),
+                                 ws.numel() * 4, B, H, Q, hd, C.c_void_p(out.data_ptr()),
+                                 C.c_void_p(current_stream_ptr()))
+    _lib.check(st, "dc_lse_merge")
+    got = out.cpu().numpy()
+    for i, (b, c) in enumerate(zip(begins, counts)):
+        s, h = divmod(i, H)
+        mm = m[b:b + c].astype(np.float64)
+        M = np.max(mm, axis=0)
+        w = np.where(np.isneginf(mm), 0.0, np.exp2(mm - np.where(np.isneginf(M), 0.0, M)))
+        L = np.sum(w * l[b:b + c], axis=0)
+        want = np.einsum("sq,sqd->qd", w, part_o[b:b + c].astype(np.float64)) / np.maximum(L, 1e-30)[:, None]
+        np.testing.assert_allclose(got[s, h], want, atol=2e-5, rtol=2e-5)
