@@ -187,7 +187,9 @@ def main():
     ms_step = timed(wl.step, args.steps) / args.steps
 
     # (2) the dominant kernel alone: the K steps' decode launches back to
-    # back (partials left in the workspace), then (3) the merges alone
+    # back (partials left in the workspace), then (3) the merges alone; each
+    # as a graph of one step's launches (unless --eager), so that a short
+    # kernel is not timed at the host's launch rate
     def decode_all():
         for l in range(L):
             wl.decode_kernel(l)
@@ -196,6 +198,9 @@ def main():
         for l in range(L):
             wl.merge_kernel(l)
 
+    if not args.eager:
+        g_dec, g_merge = wl.capture_fn(decode_all), wl.capture_fn(merge_all)
+        decode_all, merge_all = g_dec.replay, g_merge.replay
     launch_ms = timed(decode_all, args.steps) / (args.steps * L)
     merge_ms = timed(merge_all, args.steps) / (args.steps * L)
 

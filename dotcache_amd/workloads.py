@@ -190,19 +190,24 @@ class Workload:
         kernels) as a HIP graph; :meth:`step` then replays it, so a decode
         loop costs one host launch per step.  Pools, tables, plan and
         buffers must not be reallocated afterwards."""
-        torch = _torch()
         self.graph = None
+        self.graph = self.capture_fn(self.step)
+
+    def capture_fn(self, fn):
+        """``fn`` (a sequence of this workload's kernel launches) captured as
+        a HIP graph, after one eager warm-up run on a side stream."""
+        torch = _torch()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):  # warm-up: descriptor tables and plan uploaded before capture
-            self.step()
+            fn()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self.step()
+            fn()
         torch.cuda.synchronize()
-        self.graph = g
+        return g
 
     def _append(self, l: int) -> None:
         """Encode this step's new K / V row of every (sequence, KV head) into
