@@ -37,6 +37,8 @@
 //          VGS g + 8 (r / L) + r % L + L h with L = 128 / VGS, which lets
 //          every lane unpack its codes with one byte permute per pair of
 //          tokens.
+#include <type_traits>
+
 #include "dc_common.h"
 #include "dc_decode.h"
 
@@ -143,6 +145,26 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // two staged chunks in flight where the registers allow it
   constexpr bool kPipe = HD <= 128 && !(VM3 && KMODE == KEYS_MIXED);
   __shared__ uint32_t lds_all[(kPipe ? 2 : 1) * Cfg::STAGE];
+  // M3-only keys at head_dim 128: each chunk's 32 key rows go straight from
+  // HBM into an LDS buffer (buffer_load ... lds), 1 KiB-contiguous per
+  // instruction, and the score reads them back in the MFMA's A layout.  Two
+  // buffers as separate objects, so a read of one waits only for its own
+  // loads.  Row t holds its 16-byte piece p at slot p ^ swz(t), swz(t) =
+  // bits {0, 1, 3, 4} of t, which puts the 16 rows one read touches in 16
+  // distinct bank groups.
+  constexpr bool kDmaK = kPipe && KMODE == KEYS_M3 && HD == 128;
+  __shared__ __attribute__((aligned(16))) uint32_t kbuf0[kDmaK ? 32 * HD / 2 : 1];
+  __shared__ __attribute__((aligned(16))) uint32_t kbuf1[kDmaK ? 32 * HD / 2 : 1];
+  // key buffer 0 or 1, chosen at compile time (std::integral_constant), so
+  // every LDS address the loads and reads use is a constant of one object
+  auto kbuf = [&](auto bi) -> uint32_t* {
+    if constexpr (decltype(bi)::value == 0)
+      return kbuf0;
+    else
+      return kbuf1;
+  };
+  using KB0 = std::integral_constant<int, 0>;
+  using KB1 = std::integral_constant<int, 1>;
 
   const dc_work_item it = a.items[blockIdx.x];
   const int lane = threadIdx.x;
@@ -151,59 +173,86 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   const int CAP = a.kpool.geometry.page_capacity;
   const bool head_live = r < nq;
 
+  // The prologue's loads go out in two rounds: the queries and the first
+  // page batch's table entries together, then the descriptors those name.
+  // Every load is unconditional (clamped index or a bounds-checked buffer
+  // resource), so no load waits on a branch.
+  // ---- queries, raw: lane (r, kb) holds channels 32 g + 8 kb + i of head r ----
+  const int64_t qbase = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * nq * HD;
+  const int64_t qrow = qbase + int64_t(head_live ? r : 0) * HD + 8 * kb;
+  const bool q_f32 = a.queries_dtype == DC_F32;
+  u32x4 qraw[2 * KG];  // fp32: two 16-byte pieces per group; fp16 / bf16: one
+  if (q_f32) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.queries) + qrow);
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      qraw[2 * g] = q[8 * g];
+      qraw[2 * g + 1] = q[8 * g + 1];
+    }
+  } else {
+    const u32x4* q = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.queries) + qrow);
+#pragma unroll
+    for (int g = 0; g < KG; ++g) qraw[g] = q[4 * g];
+  }
+
   // ---- page metadata: lane i holds the ids / descriptors of page begin + base + i ----
   const int64_t trow = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * a.table_stride;
   const int np = it.page_end - it.page_begin;
+  const int kn = a.kpool.n_descs, vn = a.vpool.n_descs;
+  // descriptor arrays as buffer resources: an id past the end reads zeros
+  const __amdgpu_buffer_rsrc_t kdr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(static_cast<const void*>(a.kpool.descs)), 0, kn < (1 << 28) ? kn * 8 : (1 << 31) - 8, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vdr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(static_cast<const void*>(a.vpool.descs)), 0, vn < (1 << 28) ? vn * 8 : (1 << 31) - 8, 0x00020000);
   uint32_t k0 = 0, k1 = 0, v0 = 0, v1 = 0;
-  int ok = 0;
-  auto load_meta = [&](int base) {
+  int ok = 0, kid = 0, vid = 0;
+  auto load_ids = [&](int base) {  // lanes past the batch re-read its last entry
     const int nb = np - base < 64 ? np - base : 64;
-    k0 = k1 = v0 = v1 = 0u;
-    ok = 0;
-    if (lane < nb) {
-      const int p = it.page_begin + base + lane;
-      const int kid = a.k_table[trow + p], vid = a.v_table[trow + p];
-      if (kid >= 0 && kid < a.kpool.n_descs && vid >= 0 && vid < a.vpool.n_descs) {
-        const uint2 kd = *reinterpret_cast<const uint2*>(a.kpool.descs + kid);
-        const uint2 vd = *reinterpret_cast<const uint2*>(a.vpool.descs + vid);
-        k0 = kd.x; k1 = kd.y; v0 = vd.x; v1 = vd.y;
-        ok = 1;
-      }
-    }
+    const int p = it.page_begin + base + (lane < nb ? lane : nb - 1);
+    kid = a.k_table[trow + p];
+    vid = a.v_table[trow + p];
+    ok = lane < nb;
   };
-  if (np > 0) load_meta(0);
+  auto load_descs = [&]() {
+    ok = ok && kid >= 0 && kid < kn && vid >= 0 && vid < vn;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 kd = __builtin_amdgcn_raw_buffer_load_b64(kdr, ok ? int(uint32_t(kid) * 8u) : -16, 0, 0);
+    const u32x2 vd = __builtin_amdgcn_raw_buffer_load_b64(vdr, ok ? int(uint32_t(vid) * 8u) : -16, 0, 0);
+    k0 = kd.x; k1 = kd.y; v0 = vd.x; v1 = vd.y;
+  };
+  if (np > 0) load_ids(0);
+  load_descs();  // unconditional: an empty item's lanes are not ok and read zeros
 
   // ---- queries scaled by query_scale * log2(e): B fragments hi / residual ----
-  // lane (r, kb) holds channels 32 g + 8 kb + i of head r
-  const int64_t qbase = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * nq * HD;
   const float qmul = a.q_scale * kLog2e;
   Frag qhi[KG], qlo[KG];
   float qsum[KG];
   {
-    const int64_t qrow = qbase + int64_t(head_live ? r : 0) * HD + 8 * kb;
     float qv[KG][8];
-    if (a.queries_dtype == DC_F32) {
-      const float* q = reinterpret_cast<const float*>(a.queries) + qrow;
+    if (q_f32) {
 #pragma unroll
-      for (int g = 0; g < KG; ++g) {
-        const float4 x0 = *reinterpret_cast<const float4*>(q + 32 * g);
-        const float4 x1 = *reinterpret_cast<const float4*>(q + 32 * g + 4);
-        qv[g][0] = x0.x; qv[g][1] = x0.y; qv[g][2] = x0.z; qv[g][3] = x0.w;
-        qv[g][4] = x1.x; qv[g][5] = x1.y; qv[g][6] = x1.z; qv[g][7] = x1.w;
-      }
-    } else {
-      const uint16_t* q = reinterpret_cast<const uint16_t*>(a.queries) + qrow;
-      const bool bf = a.queries_dtype == DC_BF16;
-#pragma unroll
-      for (int g = 0; g < KG; ++g) {
-        const uint4 x = *reinterpret_cast<const uint4*>(q + 32 * g);
-        const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+      for (int g = 0; g < KG; ++g)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          qv[g][2 * i] = bf ? __uint_as_float(xs[i] << 16) : float(h2_of(xs[i])[0]);
-          qv[g][2 * i + 1] = bf ? __uint_as_float(xs[i] & 0xffff0000u) : float(h2_of(xs[i])[1]);
+          qv[g][i] = __uint_as_float(qraw[2 * g][i]);
+          qv[g][4 + i] = __uint_as_float(qraw[2 * g + 1][i]);
         }
-      }
+    } else if (a.queries_dtype == DC_BF16) {
+#pragma unroll
+      for (int g = 0; g < KG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[g][2 * i] = __uint_as_float(qraw[g][i] << 16);
+          qv[g][2 * i + 1] = __uint_as_float(qraw[g][i] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+      for (int g = 0; g < KG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[g][2 * i] = float(h2_of(qraw[g][i])[0]);
+          qv[g][2 * i + 1] = float(h2_of(qraw[g][i])[1]);
+        }
     }
 #pragma unroll
     for (int g = 0; g < KG; ++g) {
@@ -273,6 +322,24 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     koff_m3[hh] = (ta * HD + 8 * kb) * 2;                     // M3 row piece, channels 8 kb .. of group 0
     koff_m0[hh] = ta * 16 + (Regs::kWordKeys ? 4 * kb : 0);  // (token, group 0) code block (or its word kb)
   }
+  // key DMA: instruction i writes rows 4 i .. 4 i + 3 of the chunk; lane l
+  // takes row 4 i + l / 16, slot l % 16, i.e. source piece (l % 16) ^
+  // swz(row) with swz(row) = l / 16 + 4 ((i / 2) % 4): one offset per pair
+  uint32_t kdma[4];
+#pragma unroll
+  for (int ip = 0; ip < 4; ++ip) {
+    const uint32_t rw = uint32_t(lane >> 4), sw = rw | uint32_t(ip << 2);
+    kdma[ip] = rw * (HD * 2) + 16u * ((uint32_t(lane) & 15u) ^ sw);
+  }
+  // score read of tile hh, group g: row ta = 8 (r / 4) + 4 hh + r % 4 (swz(ta) = r), piece 4 g + kb
+  uint32_t krd[2][KG];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
+      krd[hh][g] = ta * (HD / 2) + 4u * ((uint32_t(4 * g + kb)) ^ uint32_t(r));  // in words
+    }
   uint32_t voff[Cfg::NVP];
 #pragma unroll
   for (int k = 0; k < Cfg::NVP; ++k) {
@@ -282,9 +349,14 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   }
   const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
-  auto load_chunk = [&](const PageMeta& m, Regs& R) {
+  auto load_chunk = [&](const PageMeta& m, Regs& R, auto kbi) {
     const int c0 = m.c0;
-    if constexpr (Regs::kWordKeys) {
+    if constexpr (kDmaK) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(m.krs, (__attribute__((address_space(3))) void*)(kbuf(kbi) + 256 * i),
+                                                 16, kdma[i >> 1], c0 * HD * 2 + 1024 * i, 0, kNT);
+    } else if constexpr (Regs::kWordKeys) {
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
@@ -352,9 +424,25 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
-  auto score_chunk = [&](const PageMeta& m, const Regs& R, const uint32_t* lds, float* Ls) {
+  auto score_chunk = [&](const PageMeta& m, const Regs& R, const uint32_t* lds, auto kbi, float* Ls) {
+    const uint32_t* kl = kbuf(kbi);
     if (key_is_m3(m)) {
-      if constexpr (!Regs::kWordKeys) {
+      if constexpr (kDmaK) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int g = 0; g < KG; ++g) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(kl + krd[hh][g]);
+            Frag ka;
+            ka.u[0] = x.x; ka.u[1] = x.y; ka.u[2] = x.z; ka.u[3] = x.w;
+            d = mfma(ka, qhi[g], d);
+            d = mfma(ka, qlo[g], d);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = d[i];
+        }
+      } else if constexpr (!Regs::kWordKeys) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           f32x4 d = {0.f, 0.f, 0.f, 0.f};
@@ -549,7 +637,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // ---- walk the pages: metadata 64 pages at a time, chunks pipelined ----
   for (int base = 0; base < np; base += 64) {
     const int nb = np - base < 64 ? np - base : 64;
-    if (base > 0) load_meta(base);
+    if (base > 0) {
+      load_ids(base);
+      load_descs();
+    }
     // lane i: everything about page base + i, once for the batch (vector
     // work instead of per-page scalar work): token count, formats, blob
     // sizes, scale / bias offsets, and its end chunk index in the batch
@@ -623,23 +714,25 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       Regs RA, RB;
       PageMeta cur = chunk_meta(0);
       PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
-      load_chunk(cur, RA);
-      load_chunk(nxt, RB);
+      load_chunk(cur, RA, KB0{});
+      load_chunk(nxt, RB, KB1{});
       float Ls[8], pa[8];
       stage_chunk(RA, buf0);
-      score_chunk(cur, RA, buf0, Ls);
+      score_chunk(cur, RA, buf0, KB0{}, Ls);
       softmax_chunk(cur, Ls, pa);
       int j = 0;
-      auto step = [&](Regs& X, Regs& Y, uint32_t* bm, uint32_t* bs) -> bool {
+      // chunk j: values in stage buffer bm (keys in km, already scored);
+      // chunk j + 1: registers X, keys in ks; chunk j + 2 loads into Y, km
+      auto step = [&](Regs& X, Regs& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) -> bool {
         if (j + 1 >= total) {  // last chunk: mix only
           mix_chunk(cur, bm, pa);
           return false;
         }
         const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : no_chunk(nxt);
-        load_chunk(n2, Y);
+        load_chunk(n2, Y, km);
         float Ln[8];
         stage_chunk(X, bs);
-        score_chunk(nxt, X, bs, Ln);
+        score_chunk(nxt, X, bs, ks, Ln);
         mix_chunk(cur, bm, pa);
         softmax_chunk(nxt, Ln, pa);
         cur = nxt;
@@ -647,18 +740,18 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         ++j;
         return true;
       };
-      while (step(RB, RA, buf0, buf1) && step(RA, RB, buf1, buf0)) {
+      while (step(RB, RA, buf0, buf1, KB0{}, KB1{}) && step(RA, RB, buf1, buf0, KB1{}, KB0{})) {
       }
     } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
       Regs R;
       PageMeta cur = chunk_meta(0);
-      load_chunk(cur, R);
+      load_chunk(cur, R, KB0{});
       for (int j = 0; j < total; ++j) {
         const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
         float Ls[8], pa[8];
         stage_chunk(R, lds_all);
-        score_chunk(cur, R, lds_all, Ls);
-        load_chunk(nm, R);
+        score_chunk(cur, R, lds_all, KB0{}, Ls);
+        load_chunk(nm, R, KB0{});
         softmax_chunk(cur, Ls, pa);
         mix_chunk(cur, lds_all, pa);
         cur = nm;
