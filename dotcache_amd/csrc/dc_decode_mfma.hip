@@ -375,22 +375,26 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         }
       }
     }
+    // the scale / bias offsets are wave-uniform; readfirstlane says so, or
+    // the compiler wraps each of these loads in a per-value loop
     if constexpr (KMODE != KEYS_M3) {
+      const int ksc = __builtin_amdgcn_readfirstlane(int(m.ksc)), kbs = __builtin_amdgcn_readfirstlane(int(m.kbs));
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
-        R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), int(m.ksc) + c0 * KG * 2 + 256 * k, kNT);
+        R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), ksc + c0 * KG * 2 + 256 * k, kNT);
         if constexpr (KAFF)
-          R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), int(m.kbs) + c0 * KG * 2 + 256 * k, kNT);
+          R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), kbs + c0 * KG * 2 + 256 * k, kNT);
       }
     }
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k)
       R.vr[k] = __builtin_amdgcn_raw_buffer_load_b128(m.vrs, int(voff[k]), c0 * W * 4, kNT);
+    const int vsc = __builtin_amdgcn_readfirstlane(int(m.vsc)), vbs = __builtin_amdgcn_readfirstlane(int(m.vbs));
 #pragma unroll
     for (int k = 0; k < Cfg::NVS; ++k) {
-      R.vs[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), int(m.vsc) + c0 * VG * 2 + 256 * k, kNT);
+      R.vs[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), vsc + c0 * VG * 2 + 256 * k, kNT);
       if constexpr (VAFF)
-        R.vb[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), int(m.vbs) + c0 * VG * 2 + 256 * k, kNT);
+        R.vb[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), vbs + c0 * VG * 2 + 256 * k, kNT);
     }
   };
 
