@@ -224,10 +224,15 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   load_descs();  // unconditional: an empty item's lanes are not ok and read zeros
 
   // ---- queries scaled by query_scale * log2(e): B fragments hi / residual ----
+  // converted once, after the item's first chunk loads are issued, so the
+  // conversion overlaps them
   const float qmul = a.q_scale * kLog2e;
   Frag qhi[KG], qlo[KG];
   float qsum[KG];
-  {
+  bool q_ready = false;
+  auto prep_queries = [&]() {
+    if (q_ready) return;
+    q_ready = true;
     float qv[KG][8];
     if (q_f32) {
 #pragma unroll
@@ -269,7 +274,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       s += __shfl_xor(s, 32, 64);
       qsum[g] = s;  // sum of group g of head r
     }
-  }
+  };
 
   // mix column of this lane in tile h of value group g: d = VGS g + dcol + LPW4 h
   const int jj = r % LPW4, w4 = r / LPW4;
@@ -302,7 +307,6 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   float neg1 = -1.f;
   asm volatile("" : "+v"(neg1));
 
-  const dc_page_geometry kgeo = a.kpool.geometry, vgeo = a.vpool.geometry;
 
   auto key_is_m3 = [&](const PageMeta& m) -> bool {
     if constexpr (KMODE == KEYS_M3) return true;
@@ -638,6 +642,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     }
   };
 
+  // head_dim 256 converts up front: holding its raw queries across the first
+  // loads would cost registers it does not have
+  if constexpr (HD > 128) prep_queries();
+
   // ---- walk the pages: metadata 64 pages at a time, chunks pipelined ----
   for (int base = 0; base < np; base += 64) {
     const int nb = np - base < 64 ? np - base : 64;
@@ -648,21 +656,25 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     // lane i: everything about page base + i, once for the batch (vector
     // work instead of per-page scalar work): token count, formats, blob
     // sizes, scale / bias offsets, and its end chunk index in the batch
-    const BlobLayout KL = blob_layout(int(k1 >> 16) & 0xff, int(k1 >> 24), kgeo);
-    const BlobLayout VL = blob_layout(int(v1 >> 16) & 0xff, int(v1 >> 24), vgeo);
+    // blob layout (dc_common.h blob_layout) of the formats this kernel
+    // accepts, from its fixed geometry: keys M3 fp16 or M0 4-bit group 32,
+    // values M3 fp16 or M0 VBITS-bit group VGS, capacity CAP
+    const int kf = int(k1 >> 16) & 0xff, vf = int(v1 >> 16) & 0xff;
+    const uint32_t cap = uint32_t(CAP), m3_bytes = cap * HD * 2;
+    const uint32_t kpay = uint32_t(KG) * cap * 16, ksb = (cap * KG * 2 + 15) & ~15u;
+    const uint32_t vpay = uint32_t(VG) * cap * W * 4, vsb = (cap * VG * 2 + 15) & ~15u;
+    const bool km0 = is_m0(kf), vm0 = is_m0(vf), kaff = kf == DC_FMT_M0_AFFINE, vaff = vf == DC_FMT_M0_AFFINE;
+    const uint32_t ksc = km0 ? kpay : 0u, kbs = kaff ? kpay + ksb : ksc;
+    const uint32_t vsc = vm0 ? vpay : 0u, vbs = vaff ? vpay + vsb : vsc;
+    const uint32_t ktot = km0 ? kpay + ksb + (kaff ? ksb : 0u) : m3_bytes;
+    const uint32_t vtot = vm0 ? vpay + vsb + (vaff ? vsb : 0u) : m3_bytes;
     int T = min(int(k1 & 0xffff), int(v1 & 0xffff));
     T = min(T, CAP);
-    if (!ok || lane >= nb || (int64_t(k0) << 8) + KL.total > a.kpool.arena_bytes ||
-        (int64_t(v0) << 8) + VL.total > a.vpool.arena_bytes)
+    if (!ok || lane >= nb || (int64_t(k0) << 8) + ktot > a.kpool.arena_bytes ||
+        (int64_t(v0) << 8) + vtot > a.vpool.arena_bytes)
       T = 0;
-    const int kf = int(k1 >> 16) & 0xff, vf = int(v1 >> 16) & 0xff;
     const uint32_t info = uint32_t(T) | (uint32_t(kf) << 16) | (uint32_t(vf) << 24);
-    const uint32_t ksc = is_m0(kf) ? uint32_t(KL.scales_off) : 0u;
-    const uint32_t kbs = kf == DC_FMT_M0_AFFINE ? uint32_t(KL.bias_off) : ksc;
-    const uint32_t vsc = is_m0(vf) ? uint32_t(VL.scales_off) : 0u;
-    const uint32_t vbs = vf == DC_FMT_M0_AFFINE ? uint32_t(VL.bias_off) : vsc;
     const uint32_t koffs = ksc | (kbs << 16), voffs = vsc | (vbs << 16);  // offsets < 64 KiB for M0 pages
-    const uint32_t ktot = uint32_t(KL.total), vtot = uint32_t(VL.total);
     const int nch = (T + 31) >> 5;  // < 16 (capacity <= 256)
     // inclusive prefix sum over the lanes (end chunk of page lane), bit by
     // bit: ballot of the bit, count of set lanes at or below this one
@@ -720,6 +732,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
       load_chunk(cur, RA, KB0{});
       load_chunk(nxt, RB, KB1{});
+      prep_queries();
       float Ls[8], pa[8];
       stage_chunk(RA, buf0);
       score_chunk(cur, RA, buf0, KB0{}, Ls);
@@ -750,6 +763,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       Regs R;
       PageMeta cur = chunk_meta(0);
       load_chunk(cur, R, KB0{});
+      prep_queries();
       for (int j = 0; j < total; ++j) {
         const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
         float Ls[8], pa[8];
