@@ -324,7 +324,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   for (int hh = 0; hh < 2; ++hh) {
     const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
     koff_m3[hh] = (ta * HD + 8 * kb) * 2;                     // M3 row piece, channels 8 kb .. of group 0
-    koff_m0[hh] = ta * 16 + (Regs::kWordKeys ? 4 * kb : 0);  // (token, group 0) code block (or its word kb)
+    // word kb of the (token, group 0) code block; a 16-byte load from there
+    // (pools with M3 keys too) has that word first and reads on inside the blob
+    koff_m0[hh] = ta * 16 + 4 * kb;
   }
   // key DMA: instruction i writes rows 4 i .. 4 i + 3 of the chunk; lane l
   // takes row 4 i + l / 16, slot l % 16, i.e. source piece (l % 16) ^
@@ -473,6 +475,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       const float bf = k_affine ? 1.f : 0.f;
       // (1024 + n_lo, 1024 + 16 n_hi) -> (n_lo - zp, n_hi - zp)
       const h2 kmul = {(_Float16)1.f, (_Float16)0.0625f};
+      float qb[KG];  // bias weight of group g: sum of the query's group g (affine pages only)
+#pragma unroll
+      for (int g = 0; g < KG; ++g) qb[g] = bf * qsum[g];
       const h2 kadd = {(_Float16)(-1024.f - zp), (_Float16)(-64.f - zp)};
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -494,7 +499,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           if constexpr (Regs::kWordKeys) {
             w = R.kw[hh][g];
           } else {
-            w = kb == 0 ? R.kr[hh][g].x : kb == 1 ? R.kr[hh][g].y : kb == 2 ? R.kr[hh][g].z : R.kr[hh][g].w;
+            w = R.kr[hh][g].x;
           }
           Frag ka;
 #pragma unroll
@@ -511,8 +516,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int e = i * KG + g;
-            Lh[i] += float(h2_of(sw[e >> 1])[e & 1]) * d[i];
-            if constexpr (KAFF) Lh[i] += bf * float(h2_of(bw[e >> 1])[e & 1]) * qsum[g];
+            // fp16 scale / bias times an fp32 value: one v_fma_mix_f32 each
+            Lh[i] = __builtin_fmaf(float(h2_of(sw[e >> 1])[e & 1]), d[i], Lh[i]);
+            if constexpr (KAFF) Lh[i] = __builtin_fmaf(float(h2_of(bw[e >> 1])[e & 1]), qb[g], Lh[i]);
           }
         }
 #pragma unroll
