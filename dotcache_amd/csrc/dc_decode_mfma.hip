@@ -572,6 +572,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       const bool v_affine = VAFF && m.vfmt == DC_FMT_M0_AFFINE;
       const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
       const float bf = v_affine ? 1.f : 0.f;
+      float pb[8];  // weights of the bias sums (0 on symmetric pages)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[e] = bf * pa[e];
       // codes become fp16 (1024 + c), or (1024 + 16 c) for a code in the high
       // nibble of its byte; one packed fma maps either to c - zp exactly
       const h2 vadd = VBITS == 4 && (jj & 1) ? h2{(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)}
@@ -599,9 +602,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           const Split2 sp = split2(x0, x1, neg1);
           fa_hi.u[pp] = sp.hi;
           fa_res.u[pp] = sp.res;
-          if constexpr (VAFF)
-            bsum[g] += bf * (pa[2 * pp] * float(h2_of(bw[e0 >> 1])[e0 & 1]) +
-                             pa[2 * pp + 1] * float(h2_of(bw[e1 >> 1])[e1 & 1]));
+          if constexpr (VAFF) {  // fp16 bias times weight: one v_fma_mix_f32 each
+            bsum[g] = __builtin_fmaf(float(h2_of(bw[e0 >> 1])[e0 & 1]), pb[2 * pp], bsum[g]);
+            bsum[g] = __builtin_fmaf(float(h2_of(bw[e1 >> 1])[e1 & 1]), pb[2 * pp + 1], bsum[g]);
+          }
         }
         const uint32_t* P = lds + Cfg::VPAY + g * Cfg::GSTRIDE + vrow;  // token 8 kb + e at P[e W]
 #pragma unroll
