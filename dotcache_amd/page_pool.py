@@ -109,7 +109,7 @@ class DevicePagePool:
         self._host_desc = np.zeros(max(int(reserve_pages), 16), dtype=DESC_DTYPE)
         self._n_pages = 0
         self._dev_desc = None
-        self._dirty = True
+        self._dirty_ids: set[int] = set()  # descriptors changed since the last device upload
         self.headers: dict[int, PageHeader] = {}
         self._blob_size: dict[int, int] = {}
         self._live = np.zeros(self._host_desc.shape[0], dtype=bool)
@@ -166,7 +166,7 @@ class DevicePagePool:
             self._live[pid] = True
             self._blob_size[pid] = nblk
             ids[i] = pid
-        self._dirty = True
+        self._dirty_ids.update(ids.tolist())
         return ids
 
     def free(self, page_ids) -> None:
@@ -179,7 +179,7 @@ class DevicePagePool:
             self._free.setdefault(nblk, []).append(int(self._host_desc[pid]["block"]))
             self._host_desc[pid] = (0, 0, 0, 0)
             self.headers.pop(pid, None)
-        self._dirty = True
+            self._dirty_ids.add(pid)
 
     def set_tokens(self, page_ids, tokens) -> None:
         ids = np.atleast_1d(np.asarray(page_ids, dtype=np.int64)).ravel()
@@ -191,7 +191,7 @@ class DevicePagePool:
             h = self.headers.get(pid)
             if h is not None:
                 h.token_count = int(t)
-        self._dirty = True
+        self._dirty_ids.update(ids.tolist())
 
     def desc(self, page_id: int):
         return self._host_desc[int(page_id)]
@@ -205,12 +205,20 @@ class DevicePagePool:
             raise ValueError("page table names a page that is not live in this pool")
 
     def device_descs(self):
-        """Device copy of the descriptor table (re-uploaded when changed)."""
+        """Device copy of the descriptor table, sized like the host table.
+        Changed descriptors are copied up by index; the whole table only
+        when the host table has outgrown the device copy."""
         torch = _torch()
-        if self._dirty or self._dev_desc is None:
-            raw = self._host_desc[: max(self._n_pages, 1)].view(np.int64).copy()
+        cap = self._host_desc.shape[0]
+        if self._dev_desc is None or self._dev_desc.numel() < cap:
+            raw = self._host_desc.view(np.int64).copy()
             self._dev_desc = torch.from_numpy(raw).to(self.device, non_blocking=False)
-            self._dirty = False
+            self._dirty_ids.clear()
+        elif self._dirty_ids:
+            ids = np.fromiter(sorted(self._dirty_ids), dtype=np.int64, count=len(self._dirty_ids))
+            vals = torch.from_numpy(self._host_desc[ids].view(np.int64).copy()).to(self.device, non_blocking=False)
+            self._dev_desc[torch.from_numpy(ids).to(self.device)] = vals
+            self._dirty_ids.clear()
         return self._dev_desc
 
     def c_pool(self) -> _lib.Pool:
@@ -290,13 +298,13 @@ class DevicePagePool:
                 self._live[pid] = True
                 self._blob_size[pid] = nblk
                 self.headers[pid] = PageHeader.from_dict(pages[i].header.to_dict())
+                self._dirty_ids.add(pid)
                 ids[i] = pid
             self._next_block = start + len(idx) * nblk
             src = torch.from_numpy(host)
             if self.device.type == "cuda":
                 src = src.pin_memory()
             self.arena[start * 256: start * 256 + host.size].copy_(src, non_blocking=False)
-        self._dirty = True
         return ids
 
     def header_of(self, page_id: int, kind: str = "K") -> PageHeader:

@@ -1,0 +1,116 @@
+"""The device KV cache lifecycle (prefill ingest, per-token append into the
+tail, page finalise, decode) against the oracle: decode outputs within the
+kernel tolerance, finalised pages bit-identical to the oracle's encode of
+the same fp32 rows (reference ``model_kv_cache.py:3609-4134``)."""
+import numpy as np
+import pytest
+
+from oracle import dotcache_oracle as O
+from tests.helpers import hard_values, pool_page_to_oracle
+
+pytestmark = pytest.mark.gpu
+
+KERNEL_TOL = 3e-4  # as in test_gpu_attention.py; the contract is 1e-3
+
+
+def _oracle_stream_pages(rows, cfg, kind, layer, head):
+    """The reference's pages of one stream of ``rows [T, hd]`` cached from
+    token 0: full pages in the layer's mode, the partial tail as an M3 page."""
+    P = cfg.tokens_per_page
+    T = rows.shape[0]
+    full = (T // P) * P
+    bits = cfg.bits_k if kind == "K" else cfg.bits_v
+    scheme = cfg.quant_scheme_k if kind == "K" else cfg.quant_scheme_v
+    mode = cfg.resolve_page_mode(kind=kind, layer_id=layer, kv_head_id=head)
+    pages = [O.encode_page(rows[s:s + P], head_dim=cfg.head_dim, group_size=cfg.group_size, kind=kind, bits=bits,
+                           mode=mode, scheme=scheme, token_start=s) for s in range(0, full, P)]
+    if T > full:
+        pages.append(O.encode_page(rows[full:], head_dim=cfg.head_dim, group_size=cfg.group_size, kind=kind, mode="M3",
+                                   token_start=full))
+    return pages
+
+
+def _check_decode(cache, keys, values, T, cfg, rng, q_map=None):
+    import torch
+
+    L, B, H = keys.shape[:3]
+    Hq = cache.num_attention_heads
+    qmap = np.arange(Hq) // (Hq // H) if q_map is None else np.asarray(q_map)
+    for layer in range(L):
+        q = (rng.normal(size=(B, Hq, cfg.head_dim)) / np.sqrt(cfg.head_dim)).astype(np.float32)
+        got = cache.decode_layer(layer, torch.from_numpy(q), q_map).cpu().numpy()
+        for b in range(B):
+            for h in range(H):
+                kp = _oracle_stream_pages(keys[layer, b, h, :T], cfg, "K", layer, h)
+                vp = _oracle_stream_pages(values[layer, b, h, :T], cfg, "V", layer, h)
+                heads = np.flatnonzero(qmap == h)
+                want = O.decode_grouped(q[b, heads][None], [kp], [vp])[0]
+                err = np.max(np.abs(got[b, heads] - want))
+                assert err < KERNEL_TOL, f"layer {layer} seq {b} head {h} after {T} tokens: max-abs error {err}"
+
+
+@pytest.mark.parametrize("page_tokens", [64, 16])
+def test_prefill_append_decode_matches_oracle(page_tokens):
+    """Prefill of two full pages and a partial tail, then appends one token
+    at a time and three at once, across two page finalisations; decode at
+    each stage.  page_tokens 64 runs the MFMA kernel, 16 the generic one."""
+    import torch
+
+    from dotcache_amd.config import DotCacheConfig
+    from dotcache_amd.kv_cache import DevicePagedKVCache
+
+    P = page_tokens
+    cfg = DotCacheConfig(head_dim=64, group_size=32, tokens_per_page=P, quant_scheme_v="symmetric",
+                         key_mode_overrides=("layer:1:kv:1=M3",))
+    L, B, H, Hq = 2, 2, 2, 4
+    rng = np.random.default_rng(P)
+    T0, T1 = 2 * P + 5, 4 * P + 2
+    keys = np.stack([hard_values(rng, T1, 64) for _ in range(L * B * H)]).reshape(L, B, H, T1, 64)
+    values = np.stack([hard_values(rng, T1, 64) for _ in range(L * B * H)]).reshape(L, B, H, T1, 64)
+    cache = DevicePagedKVCache(cfg, num_hidden_layers=L, num_attention_heads=Hq, num_key_value_heads=H, batch_size=B)
+    for layer in range(L):
+        cache.ingest_prefill_cache(layer, torch.from_numpy(keys[layer, :, :, :T0]), values[layer, :, :, :T0])
+    _check_decode(cache, keys, values, T0, cfg, rng)
+    t = T0
+    while t < T1:
+        n = 3 if t == T0 + 4 else 1
+        for layer in range(L):
+            cache.append_step(layer, keys[layer, :, :, t:t + n], torch.from_numpy(values[layer, :, :, t:t + n]), t)
+        t += n
+        if t in (3 * P - 1, 3 * P, 3 * P + 1, T1):
+            _check_decode(cache, keys, values, t, cfg, rng)
+    assert cache.sequence_length(0) == T1
+    # finalised pages: bit-identical to the oracle's encode of the same fp32 rows
+    for layer in range(L):
+        for b in range(B):
+            for h in range(H):
+                for kind, src in (("K", keys), ("V", values)):
+                    want = _oracle_stream_pages(src[layer, b, h, :T1], cfg, kind, layer, h)
+                    ids = cache.page_ids(layer, b, h, kind)
+                    assert len(ids) == T1 // P
+                    pool = cache.k_pool if kind == "K" else cache.v_pool
+                    for pid, wp in zip(ids, want):
+                        gp = pool_page_to_oracle(pool, pid, kind)
+                        for f in ("payload", "scales", "bias", "escape_payload"):
+                            a, e = getattr(gp, f), getattr(wp, f)
+                            assert (a is None) == (e is None), f
+                            if a is not None:
+                                np.testing.assert_array_equal(a, e, err_msg=f"{kind} page {pid} {f}")
+
+
+def test_decode_with_a_permuted_head_map():
+    import torch
+
+    from dotcache_amd.config import DotCacheConfig
+    from dotcache_amd.kv_cache import DevicePagedKVCache
+
+    cfg = DotCacheConfig(head_dim=128, group_size=32, tokens_per_page=64)
+    L, B, H, Hq, T = 1, 1, 2, 6, 150
+    rng = np.random.default_rng(3)
+    keys = hard_values(rng, H * T, 128).reshape(L, B, H, T, 128)
+    values = hard_values(rng, H * T, 128).reshape(L, B, H, T, 128)
+    cache = DevicePagedKVCache(cfg, num_hidden_layers=L, num_attention_heads=Hq, num_key_value_heads=H, batch_size=B)
+    cache.ingest_prefill_cache(0, torch.from_numpy(keys[0, 0]), torch.from_numpy(values[0, 0]))
+    _check_decode(cache, keys, values, T, cfg, rng, q_map=[1, 0, 0, 1, 1, 0])
+    with pytest.raises(ValueError):
+        cache.decode_layer(0, torch.zeros(1, Hq, 128), [0, 0, 0, 0, 1, 1])
