@@ -49,3 +49,25 @@ def test_shapes_and_layers_are_checked():
         c.decode_layer(1, np.zeros((4, 64), np.float32))
     with pytest.raises(ValueError):
         c.ingest_prefill_cache(0, np.zeros((2, 4, 64), np.float32), np.zeros((2, 4, 64), np.float32), context_length=3)
+
+
+def test_block_cache_checks_before_device_work():
+    from dotcache_amd.block_cache import DeviceVllmPagedKVCache
+
+    cfg = DotCacheConfig(head_dim=32, group_size=32, tokens_per_page=4)
+    with pytest.raises(ValueError, match="block_size"):
+        DeviceVllmPagedKVCache(config=cfg, num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+                               block_size=8, device="cpu")
+    c = DeviceVllmPagedKVCache(config=cfg, num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2,
+                               block_size=4, device="cpu")
+    rows = np.zeros((1, 2, 32), np.float32)
+    with pytest.raises(ValueError, match="out of order"):
+        c.write_slots(0, rows, rows, [7 * 4 + 2])  # offset 2 of an empty block
+    with pytest.raises(ValueError):
+        c.write_slots(0, rows, rows, [0, 1])  # one slot per row
+    with pytest.raises(ValueError, match="unique"):
+        c.sync_layer_blocks(0, np.zeros((2, 2, 4, 32)), np.zeros((2, 2, 4, 32)), block_ids=[3, 3])
+    with pytest.raises(ValueError, match="no cached tokens"):
+        c.decode_layer(0, np.zeros((4, 32), np.float32))
+    with pytest.raises(ValueError, match="expected token_index 0"):
+        c.append_step(0, np.zeros((2, 1, 32)), np.zeros((2, 1, 32)), 4)
