@@ -243,3 +243,36 @@ def test_lse_merge_matches_float64(hd):
         L = np.sum(w * l[b:b + c], axis=0)
         want = np.einsum("sq,sqd->qd", w, part_o[b:b + c].astype(np.float64)) / np.maximum(L, 1e-30)[:, None]
         np.testing.assert_allclose(got[s, h], want, atol=2e-5, rtol=2e-5)
+
+
+@pytest.mark.parametrize("path", ["auto", "generic"])
+@pytest.mark.parametrize("kfmt,vfmt,vgs", [
+    (dict(mode="M3"), dict(bits=4, scheme="symmetric"), 32),   # config 3 formats (keys through LDS)
+    (dict(bits=4), dict(bits=8, scheme="symmetric"), 64),      # config 4 formats
+])
+def test_items_longer_than_one_metadata_batch(kfmt, vfmt, vgs, path):
+    """Items of more than 64 pages: the kernels read page metadata 64 pages
+    at a time, so these items walk a second batch.  One sequence also has
+    an empty page (0 tokens) in the middle of its list."""
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+    from dotcache_amd.decode import set_decode_path
+
+    set_decode_path(path)
+    rng = np.random.default_rng(130 + vgs)
+    hd, Q, tpp = 128, 7, 64
+    lens = [130 * tpp - 9, 70 * tpp]
+    qs = (rng.normal(size=(len(lens), Q, hd)) / np.sqrt(hd)).astype(np.float32)
+    kpg = [_pages(hard_values(rng, n, hd), tpp, hd, 32, "K", kfmt) for n in lens]
+    vpg = [_pages(hard_values(rng, n, hd), tpp, hd, vgs, "V", vfmt) for n in lens]
+    # an empty page inside sequence 1: the same page with no tokens
+    empty_k = O.encode_page(np.zeros((0, hd), np.float32), head_dim=hd, group_size=32, kind="K", **kfmt)
+    empty_v = O.encode_page(np.zeros((0, hd), np.float32), head_dim=hd, group_size=vgs, kind="V", **vfmt)
+    kpg[1].insert(40, empty_k)
+    vpg[1].insert(40, empty_v)
+    want = O.decode_grouped(qs, kpg, vpg)
+    kp = [[to_product_page(p) for p in g] for g in kpg]
+    vp = [[to_product_page(p) for p in g] for g in vpg]
+    for pps in (100, 71):  # one item of 100 / 71 pages per sequence, plus a remainder
+        got = fused(list(qs), kp, vp, pages_per_split=pps).cpu().numpy()
+        err = np.max(np.abs(got - want))
+        assert err < KERNEL_TOL, f"path {path} pps {pps}: max-abs error {err}"
