@@ -625,7 +625,11 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         }
       }
     } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): gather columns from the rows
-      const uint16_t* V = reinterpret_cast<const uint16_t*>(m.vp);
+      // 16-bit buffer loads against a resource covering the page's valid
+      // rows only: a row at or past the token count reads zero, with no branch
+      const __amdgpu_buffer_rsrc_t vrows =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0, m.T * HD * 2, 0x00020000);
+      const uint32_t vbase = uint32_t(((m.c0 + 8 * kb) * HD + dcol) * 2);  // token 8 kb, column dcol of the chunk
       Frag fa_hi, fa_res;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
@@ -637,13 +641,12 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       for (int g = 0; g < VG; ++g)
 #pragma unroll
         for (int h = 0; h < H; ++h) {
-          const int d = VGS * g + dcol + LPW4 * h;
+          const int dofs = (VGS * g + LPW4 * h) * 2;
           Frag fb;
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            const int t0 = m.c0 + 8 * kb + 2 * pp;
-            const uint32_t lo = t0 < m.T ? V[t0 * HD + d] : 0u;
-            const uint32_t hi = t0 + 1 < m.T ? V[(t0 + 1) * HD + d] : 0u;
+            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(vrows, int(vbase), (2 * pp) * HD * 2 + dofs, 0);
+            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(vrows, int(vbase), (2 * pp + 1) * HD * 2 + dofs, 0);
             fb.u[pp] = lo | (hi << 16);
           }
           acc[g * H + h] = mfma(fa_hi, fb, acc[g * H + h]);
