@@ -153,6 +153,8 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // bits {0, 1, 3, 4} of t, which puts the 16 rows one read touches in 16
   // distinct bank groups.
   constexpr bool kDmaK = kPipe && KMODE == KEYS_M3 && HD == 128;
+  // pools with M0 keys order each lane's 8 channels as pairs (i, i + 4)
+  constexpr bool kPairedQ = KMODE != KEYS_M3;
   __shared__ __attribute__((aligned(16))) uint32_t kbuf0[kDmaK ? 32 * HD / 2 : 1];
   __shared__ __attribute__((aligned(16))) uint32_t kbuf1[kDmaK ? 32 * HD / 2 : 1];
   // key buffer 0 or 1, chosen at compile time (std::integral_constant), so
@@ -264,7 +266,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x0 = head_live ? qv[g][2 * i] * qmul : 0.f, x1 = head_live ? qv[g][2 * i + 1] * qmul : 0.f;
+        // k-slot pair i: channels (2i, 2i + 1) of the lane's 8, or (i, i + 4)
+        // where M0 keys occur (the order their nibble unpack produces)
+        const int c0 = kPairedQ ? i : 2 * i, c1 = kPairedQ ? i + 4 : 2 * i + 1;
+        const float x0 = head_live ? qv[g][c0] * qmul : 0.f, x1 = head_live ? qv[g][c1] * qmul : 0.f;
         qhi[g].u[i] = pack_h2(x0, x1);
         const h2 hv = h2_of(qhi[g].u[i]);
         qlo[g].u[i] = pack_h2(x0 - float(hv[0]), x1 - float(hv[1]));
@@ -306,6 +311,11 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   float m_ref = -INFINITY, l_part = 0.f;
   float neg1 = -1.f;
   asm volatile("" : "+v"(neg1));
+  // the fp16 magic 0x6400 pair, held in a VGPR the compiler cannot see
+  // through: (w & mask) | magic with a scalar mask is then one v_and_or_b32
+  // (a VOP3 here takes no literal and at most one scalar operand)
+  uint32_t fp16_magic = 0x64006400u;
+  asm volatile("" : "+v"(fp16_magic));
 
 
   auto key_is_m3 = [&](const PageMeta& m) -> bool {
@@ -459,7 +469,15 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
           for (int g = 0; g < KG; ++g) {
             Frag ka;
-            ka.u[0] = R.kr[hh][g].x; ka.u[1] = R.kr[hh][g].y; ka.u[2] = R.kr[hh][g].z; ka.u[3] = R.kr[hh][g].w;
+            const u32x4 x = R.kr[hh][g];  // channels (0, 1), (2, 3), (4, 5), (6, 7)
+            if constexpr (kPairedQ) {        // -> (0, 4), (1, 5), (2, 6), (3, 7)
+              ka.u[0] = __builtin_amdgcn_perm(x.z, x.x, 0x05040100u);
+              ka.u[1] = __builtin_amdgcn_perm(x.z, x.x, 0x07060302u);
+              ka.u[2] = __builtin_amdgcn_perm(x.w, x.y, 0x05040100u);
+              ka.u[3] = __builtin_amdgcn_perm(x.w, x.y, 0x07060302u);
+            } else {
+              ka.u[0] = x.x; ka.u[1] = x.y; ka.u[2] = x.z; ka.u[3] = x.w;
+            }
             d = mfma(ka, qhi[g], d);
             d = mfma(ka, qlo[g], d);
           }
@@ -473,12 +491,13 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       const bool k_affine = KAFF && m.kfmt == DC_FMT_M0_AFFINE;
       const float zp = k_affine ? 0.f : 7.f;
       const float bf = k_affine ? 1.f : 0.f;
-      // (1024 + n_lo, 1024 + 16 n_hi) -> (n_lo - zp, n_hi - zp)
-      const h2 kmul = {(_Float16)1.f, (_Float16)0.0625f};
       float qb[KG];  // bias weight of group g: sum of the query's group g (affine pages only)
 #pragma unroll
       for (int g = 0; g < KG; ++g) qb[g] = bf * qsum[g];
-      const h2 kadd = {(_Float16)(-1024.f - zp), (_Float16)(-64.f - zp)};
+      // (1024 + n, 1024 + n') -> (n - zp, n' - zp); (1024 + 16 n, ..) / 16 - 64 - zp likewise
+      const h2 kadd0 = {(_Float16)(-1024.f - zp), (_Float16)(-1024.f - zp)};
+      const h2 kadd1 = {(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)};
+      const h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         // scales / biases of the D-row tokens 8 kb + 4 hh + i, all groups: [4][KG] fp16
@@ -501,13 +520,16 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           } else {
             w = R.kr[hh][g].x;
           }
+          // nibble i of the word is channel i; channels i and i + 4 sit 16
+          // bits apart, so one mask and the fp16 magic 0x6400 give the pair
+          // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
+          // (nibbles 1, 3), and one packed add / fma makes it n - zp exactly
           Frag ka;
-#pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            // byte p holds channel 2p (low nibble) and 2p + 1 (high nibble)
-            const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0c040c00u + 0x00010001u * p);
-            ka.u[p] = bits_of(h2_of((x & 0x00f0000fu) | 0x64006400u) * kmul + kadd);
-          }
+          const uint32_t w8 = w >> 8;
+          ka.u[0] = bits_of(h2_of((w & 0x000f000fu) | fp16_magic) + kadd0);
+          ka.u[1] = bits_of(h2_of((w & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+          ka.u[2] = bits_of(h2_of((w8 & 0x000f000fu) | fp16_magic) + kadd0);
+          ka.u[3] = bits_of(h2_of((w8 & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
           f32x4 d = {0.f, 0.f, 0.f, 0.f};
           d = mfma(ka, qhi[g], d);
           d = mfma(ka, qlo[g], d);
