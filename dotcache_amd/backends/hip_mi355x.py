@@ -77,6 +77,15 @@ class PreparedPageHIP:
         return self.pool.blob_bytes(*page_format_of(self.header.mode_default, self.header.quant_scheme,
                                                     self.header.bits, self.header.escape_dtype))
 
+    def __del__(self) -> None:
+        # the blob goes back to its pool with the last reference, as a torch
+        # page's tensors do; work already queued on the stream still reads it
+        # first (a later upload into the slot is ordered after it)
+        try:
+            self.pool.free(self.page_id)
+        except Exception:  # interpreter shutdown, or the pool released it already
+            pass
+
 
 PageLike = EncodedPage | PreparedPageHIP
 
@@ -179,7 +188,6 @@ def prepare_pages_hip(pages: Sequence[PageLike], *, trace: ExecutionTrace | None
                                      host_to_device_nbytes=nbytes)
             if trace is not None:
                 trace.record_host_to_device(nbytes)
-                trace.prepared_page_cache_misses += 1
     return out  # type: ignore[return-value]
 
 

@@ -21,6 +21,7 @@ in ``libdotcache_hip.so``.
 from __future__ import annotations
 
 import ctypes as C
+from collections import deque
 from dataclasses import dataclass
 
 import numpy as np
@@ -90,9 +91,11 @@ class DevicePagePool:
     """Arena + descriptor table on one device.
 
     ``reserve_bytes`` sizes the arena up front; it grows (by re-allocation
-    and a device copy) when a batch of pages does not fit.  Page ids are
-    stable for the life of the pool; freed blobs are reused by later pages
-    of the same blob size.
+    and a device copy) when a batch of pages does not fit.  A page keeps its
+    id while it is live; freed blobs and freed ids are reused by later pages
+    (blobs of the same size, ids oldest-freed first), so a pool whose pages
+    come and go stays the size of its live set.  Reuse is ordered on the
+    current stream: work queued before a free still reads the old page.
     """
 
     def __init__(self, geometry: PoolGeometry, *, device="cuda", reserve_bytes: int = 64 << 20, reserve_pages: int = 4096):
@@ -108,6 +111,7 @@ class DevicePagePool:
         self._free: dict[int, list[int]] = {}
         self._host_desc = np.zeros(max(int(reserve_pages), 16), dtype=DESC_DTYPE)
         self._n_pages = 0
+        self._free_ids: deque[int] = deque()
         self._dev_desc = None
         self._dirty_ids: set[int] = set()  # descriptors changed since the last device upload
         self.headers: dict[int, PageHeader] = {}
@@ -134,6 +138,8 @@ class DevicePagePool:
         self.arena = new
 
     def _new_id(self) -> int:
+        if self._free_ids:
+            return self._free_ids.popleft()
         if self._n_pages == self._host_desc.shape[0]:
             grown = np.zeros(2 * self._host_desc.shape[0], dtype=DESC_DTYPE)
             grown[: self._n_pages] = self._host_desc[: self._n_pages]
@@ -180,6 +186,7 @@ class DevicePagePool:
             self._host_desc[pid] = (0, 0, 0, 0)
             self.headers.pop(pid, None)
             self._dirty_ids.add(pid)
+            self._free_ids.append(pid)
 
     def set_tokens(self, page_ids, tokens) -> None:
         ids = np.atleast_1d(np.asarray(page_ids, dtype=np.int64)).ravel()
@@ -286,25 +293,34 @@ class DevicePagePool:
             self._check_page_geometry(p)
             by_fmt.setdefault(page_format_of(p.header.mode_default, p.header.quant_scheme, p.header.bits, p.header.escape_dtype), []).append(i)
         for (fmt, bits), idx in by_fmt.items():
-            # fresh contiguous blocks: bypass the free list for a single copy
             nblk = self.blob_bytes(fmt, bits) // 256
-            start = self._next_block
-            self._ensure_arena(start + len(idx) * nblk)
             host = np.concatenate([self._blob_from_page(pages[i], fmt, bits) for i in idx])
-            for j, i in enumerate(idx):
+            src = torch.from_numpy(host)
+            if self.device.type == "cuda":
+                src = src.pin_memory()
+            free = self._free.get(nblk, [])
+            n_old = min(len(free), len(idx))
+            blocks = [free.pop() for _ in range(n_old)]
+            start = self._next_block
+            self._ensure_arena(start + (len(idx) - n_old) * nblk)
+            blocks += [start + j * nblk for j in range(len(idx) - n_old)]
+            self._next_block = start + (len(idx) - n_old) * nblk
+            for i, block in zip(idx, blocks):
                 pid = self._new_id()
-                self._host_desc[pid] = (start + j * nblk, pages[i].header.token_count, fmt, bits)
+                self._host_desc[pid] = (block, pages[i].header.token_count, fmt, bits)
                 self.format_mask |= _lib.format_bit(fmt, bits)
                 self._live[pid] = True
                 self._blob_size[pid] = nblk
                 self.headers[pid] = PageHeader.from_dict(pages[i].header.to_dict())
                 self._dirty_ids.add(pid)
                 ids[i] = pid
-            self._next_block = start + len(idx) * nblk
-            src = torch.from_numpy(host)
-            if self.device.type == "cuda":
-                src = src.pin_memory()
-            self.arena[start * 256: start * 256 + host.size].copy_(src, non_blocking=False)
+            if n_old == 0:  # fresh contiguous blocks: one copy
+                self.arena[start * 256: start * 256 + host.size].copy_(src, non_blocking=False)
+            else:  # one upload, then a scatter of 256-byte rows into the reused blobs
+                staged = src.to(self.device, non_blocking=False).view(-1, 256)
+                rows = (np.asarray(blocks, dtype=np.int64)[:, None] + np.arange(nblk)).ravel()
+                used = self.arena[: self._next_block * 256].view(-1, 256)
+                used.index_copy_(0, torch.from_numpy(rows).to(self.device), staged)
         return ids
 
     def header_of(self, page_id: int, kind: str = "K") -> PageHeader:

@@ -21,6 +21,9 @@ class ExecutionTrace:
     host_to_device_bytes: int = 0
     prepared_page_cache_hits: int = 0
     prepared_page_cache_misses: int = 0
+    cache_resident_bytes: int = 0
+    prepared_page_cache_evictions: int = 0
+    cache_evicted_bytes: int = 0
     calls: Counter = field(default_factory=Counter)
 
     def record_page_read(self, payload_bytes: int, metadata_bytes: int) -> None:
@@ -36,6 +39,20 @@ class ExecutionTrace:
     def record_call(self, name: str) -> None:
         self.calls[name] += 1
 
+    # prepared-page cache counters (reference tracing.py:82-93)
+    def record_cache_hit(self, count: int = 1) -> None:
+        self.prepared_page_cache_hits += int(count)
+
+    def record_cache_miss(self, count: int = 1) -> None:
+        self.prepared_page_cache_misses += int(count)
+
+    def observe_cache_resident_bytes(self, nbytes: int) -> None:
+        self.cache_resident_bytes = max(self.cache_resident_bytes, int(nbytes))
+
+    def record_cache_eviction(self, nbytes: int, count: int = 1) -> None:
+        self.prepared_page_cache_evictions += int(count)
+        self.cache_evicted_bytes += int(nbytes)
+
     @property
     def total_bytes_read(self) -> int:
         return self.payload_bytes_read + self.metadata_bytes_read
@@ -48,5 +65,8 @@ class ExecutionTrace:
             "host_to_device_bytes": self.host_to_device_bytes,
             "prepared_page_cache_hits": self.prepared_page_cache_hits,
             "prepared_page_cache_misses": self.prepared_page_cache_misses,
+            "cache_resident_bytes": self.cache_resident_bytes,
+            "prepared_page_cache_evictions": self.prepared_page_cache_evictions,
+            "cache_evicted_bytes": self.cache_evicted_bytes,
             "calls": dict(self.calls),
         }
