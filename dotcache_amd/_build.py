@@ -26,7 +26,11 @@ COMMON = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
-PER_FILE = {"dc_encode.hip": ["-ffp-contract=off"]}
+# dc_decode_mfma.hip: MFMA results in VGPRs (the VGPR form of the
+# instruction) instead of AGPRs, so the score's per-group results and the
+# softmax rescale of the accumulators need no AGPR <-> VGPR copies.
+PER_FILE = {"dc_encode.hip": ["-ffp-contract=off"],
+            "dc_decode_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _hipcc() -> str:
