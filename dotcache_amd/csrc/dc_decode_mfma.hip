@@ -232,7 +232,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   Frag qhi[KG], qlo[KG];
   float qsum[KG];
   bool q_ready = false;
-  auto prep_queries = [&]() {
+  // (the per-chunk lambdas are always inlined: at head_dim 256 the compiler
+  // otherwise calls some of them, passing the register sets through scratch)
+  auto prep_queries = [&]() __attribute__((always_inline)) {
     if (q_ready) return;
     q_ready = true;
     float qv[KG][8];
@@ -365,7 +367,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   }
   const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
-  auto load_chunk = [&](const PageMeta& m, Regs& R, auto kbi) {
+  auto load_chunk = [&](const PageMeta& m, Regs& R, auto kbi) __attribute__((always_inline)) {
     const int c0 = m.c0;
     if constexpr (kDmaK) {
 #pragma unroll
@@ -415,7 +417,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- registers -> an LDS stage buffer: value codes in padded rows, scales as loaded ([32][G] fp16) ----
-  auto stage_chunk = [&](const Regs& R, uint32_t* lds) {
+  auto stage_chunk = [&](const Regs& R, uint32_t* lds) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k) {
       const int e = lane + 64 * k;
@@ -444,7 +446,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
-  auto score_chunk = [&](const PageMeta& m, const Regs& R, const uint32_t* lds, auto kbi, float* Ls) {
+  auto score_chunk = [&](const PageMeta& m, const Regs& R, const uint32_t* lds, auto kbi, float* Ls) __attribute__((always_inline)) {
     const uint32_t* kl = kbuf(kbi);
     if (key_is_m3(m)) {
       if constexpr (kDmaK) {
@@ -550,7 +552,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- online softmax of one scored chunk: weights pa of head r on tokens 8 kb + e ----
-  auto softmax_chunk = [&](const PageMeta& m, float* Ls, float* pa) {
+  auto softmax_chunk = [&](const PageMeta& m, float* Ls, float* pa) __attribute__((always_inline)) {
     if (m.c0 + 32 > m.T) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -587,7 +589,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- mix of one staged chunk with its weights ----
-  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa) {
+  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa) __attribute__((always_inline)) {
     bool v_m0 = true;
     if constexpr (VM3) v_m0 = is_m0(m.vfmt);
     if (v_m0) {
@@ -726,12 +728,12 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     // chunk j lies in the first page whose end chunk exceeds j
     // a chunk past the end: the same loads against empty buffer resources,
     // which return zeros without touching memory
-    auto no_chunk = [&](PageMeta m) -> PageMeta {
+    auto no_chunk = [&](PageMeta m) __attribute__((always_inline)) -> PageMeta {
       m.krs = __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0x00020000);
       m.vrs = m.krs;
       return m;
     };
-    auto chunk_meta = [&](int j) -> PageMeta {
+    auto chunk_meta = [&](int j) __attribute__((always_inline)) -> PageMeta {
       const int i = __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
       PageMeta m;
       // blob pointers stay derived from the arena arguments (global memory)
@@ -775,7 +777,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       int j = 0;
       // chunk j: values in stage buffer bm (keys in km, already scored);
       // chunk j + 1: registers X, keys in ks; chunk j + 2 loads into Y, km
-      auto step = [&](Regs& X, Regs& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) -> bool {
+      auto step = [&](Regs& X, Regs& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) __attribute__((always_inline)) -> bool {
         if (j + 1 >= total) {  // last chunk: mix only
           mix_chunk(cur, bm, pa);
           return false;
