@@ -61,6 +61,37 @@ def test_workspace_reused_across_plans():
     _check(wl, 0, [(b, h) for b in range(3) for h in range(H)])
 
 
+def test_full_size_c4_sampled_streams():
+    """Config 4 at its full shape (64 ragged sequences of 256..32768 tokens,
+    per-(layer, KV head) key modes, int8 values, one layer): the longest and
+    the shortest sequence's streams against the oracle."""
+    import torch
+
+    from dotcache_amd.workloads import build_workload
+
+    wl = build_workload("c4", seed=0, layers=1)
+    wl.step()
+    torch.cuda.synchronize()
+    sp = np.asarray(wl.layers[0].seq_pages)
+    b_long, b_short = int(np.argmax(sp)), int(np.argmin(sp))
+    print(f"c4 full: sequences {b_long} ({sp[b_long]} pages) and {b_short} ({sp[b_short]} pages)", flush=True)
+    _check(wl, 0, [(b_long, 0), (b_long, 1), (b_short, 1)])
+
+
+def test_full_size_c5_sampled_stream():
+    """Config 5 at its full shape (4 x 131072 tokens, head_dim 256, the
+    appended token and the fp16 recent window, one layer): one stream
+    against the oracle."""
+    import torch
+
+    from dotcache_amd.workloads import build_workload
+
+    wl = build_workload("c5", seed=0, layers=1)
+    wl.step()
+    torch.cuda.synchronize()
+    _check(wl, 0, [(3, 2)])
+
+
 def test_full_size_c3_sampled_streams():
     """Config 3 at its full shape (batch 8 x 16384 tokens, hd 128, GQA 7,
     one layer): streams of the first and last sequence against the oracle."""
