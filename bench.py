@@ -40,8 +40,12 @@ def parse():
     ap.add_argument("--pages-per-split", type=int, default=None)
     ap.add_argument("--contiguous-pages", action="store_true",
                     help="keep each sequence's pages in allocation order instead of scattering them over the pool")
-    ap.add_argument("--decode-path", default="auto", choices=["auto", "generic"],
-                    help="auto: the MFMA kernel where the pages fit it; generic: the VALU kernel only")
+    ap.add_argument("--decode-path", default="auto", choices=["auto", "generic", "mfma"],
+                    help="auto: the MFMA kernel where the pages fit it; generic: the VALU kernel only; "
+                         "mfma: the MFMA kernel only (an error where it does not fit)")
+    ap.add_argument("--key-bits", type=int, default=None,
+                    help="re-code the configuration's M0 key pages at this width (a variant, not the "
+                         "configuration's own line)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from Python each step instead of replaying captured HIP graphs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -156,7 +160,7 @@ def main():
     log(f"building workload {args.config} ...")
     set_decode_path(args.decode_path)
     wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
-                        scatter_pages=not args.contiguous_pages)
+                        scatter_pages=not args.contiguous_pages, key_bits=args.key_bits)
     spec = wl.spec
     log(f"built in {time.time() - t0:.1f} s: {wl.plan.n_items} work items/layer, pages/split {wl.plan.pages_per_split}, "
         f"K pool {wl.k_pool.arena.numel() / 1e9:.2f} GB, V pool {wl.v_pool.arena.numel() / 1e9:.2f} GB")

@@ -44,7 +44,8 @@ def build(verbose: bool = False) -> Path:
     hipcc = _hipcc()
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
-    objs = []
+    # one hipcc per source, all at once (they are independent)
+    jobs = []
     for name in SOURCES:
         src = CSRC / name
         if not src.exists():
@@ -54,12 +55,18 @@ def build(verbose: bool = False) -> Path:
         cmd = [hipcc, *COMMON, *PER_FILE.get(name, []), *lang, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {name}:\n{res.stdout}\n{res.stderr}")
-        if verbose and res.stderr.strip():
-            print(res.stderr, file=sys.stderr)
+        proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+        jobs.append((name, obj, proc))
+    objs, failed = [], []
+    for name, obj, proc in jobs:
+        out, err = proc.communicate()
+        if proc.returncode != 0:
+            failed.append(f"hipcc failed on {name}:\n{out}\n{err}")
+        elif verbose and err.strip():
+            print(err, file=sys.stderr)
         objs.append(str(obj))
+    if failed:
+        raise RuntimeError("\n".join(failed))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -144,11 +144,14 @@ def _capacity(token_count: int) -> int:
     return max(64, 1 << (max(int(token_count), 1) - 1).bit_length())
 
 
-def pool_for(head_dim: int, group_size: int, capacity: int, layout: str, device=None) -> DevicePagePool:
-    """The module-level pool for one page geometry (created on first use)."""
+def pool_for(head_dim: int, group_size: int, capacity: int, layout: str, device=None, kind: str = "K") -> DevicePagePool:
+    """The module-level pool for one page geometry and kind (created on
+    first use).  Key and value pages live in separate pools, so a pool's
+    format mask names the formats of one role only and the decode kernel
+    is chosen for the key and value formats actually present."""
     torch = _torch()
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    key = (head_dim, group_size, capacity, layout, str(dev))
+    key = (head_dim, group_size, capacity, layout, str(dev), kind)
     pool = _pools.get(key)
     if pool is None:
         pool = DevicePagePool(PoolGeometry(head_dim, group_size, capacity, layout), device=dev)
@@ -175,11 +178,11 @@ def prepare_pages_hip(pages: Sequence[PageLike], *, trace: ExecutionTrace | None
         if not page_supported_hip(src):
             raise ValueError("page is unsupported by hip_mi355x in this phase")
         h = src.header
-        key = (h.head_dim, h.group_size, h.layout)
+        key = (h.head_dim, h.group_size, h.layout, h.kind)
         todo.setdefault(key, []).append(i)
-    for (hd, gs, layout), idx in todo.items():
+    for (hd, gs, layout, kind), idx in todo.items():
         cap = _capacity(max(_source(pages[i]).header.token_count for i in idx))
-        target = pool if pool is not None else pool_for(hd, gs, cap, layout)
+        target = pool if pool is not None else pool_for(hd, gs, cap, layout, kind=kind)
         srcs = [_source(pages[i]) for i in idx]
         ids = target.upload_pages(srcs)
         for i, pid, src in zip(idx, ids.tolist(), srcs):
@@ -211,7 +214,7 @@ def _one_pool(pages: Sequence[PageLike], trace=None) -> tuple[DevicePagePool, np
 def _one_pool_with_capacity(pages, capacity: int, trace=None):
     src = [_source(p) for p in pages]
     h = src[0].header
-    pool = pool_for(h.head_dim, h.group_size, capacity, h.layout)
+    pool = pool_for(h.head_dim, h.group_size, capacity, h.layout, kind=h.kind)
     prepared = prepare_pages_hip(src, trace=trace, pool=pool)
     return pool, np.asarray([p.page_id for p in prepared], dtype=np.int32), prepared
 
@@ -329,21 +332,20 @@ def _pair_pools(key_pages, value_pages, trace):
         raise ValueError("key_pages and value_pages must contain the same number of pages")
     if not key_pages:
         raise ValueError("decode_step requires at least one page")
-    pool, ids, prepared = _one_pool(list(key_pages) + list(value_pages), trace)
-    n = len(key_pages)
-    kid, vid = ids[:n], ids[n:]
-    if not np.array_equal(pool.tokens_of(kid), pool.tokens_of(vid)):
+    kpool, kid, kprep = _one_pool(key_pages, trace)
+    vpool, vid, vprep = _one_pool(value_pages, trace)
+    if not np.array_equal(kpool.tokens_of(kid), vpool.tokens_of(vid)):
         raise ValueError("key and value pages must hold the same token counts")
-    return pool, kid, vid, prepared
+    return kpool, vpool, kid, vid, kprep + vprep
 
 
 def decode_multi_query_step_hip_tensor(query_slices, key_pages, value_pages, *, precomputed_page_logits=None,
                                        trace: ExecutionTrace | None = None):
     """(logits [Q, T], weights [Q, T], output [Q, head_dim]) as device tensors."""
     torch = _torch()
-    pool, kid, vid, prepared = _pair_pools(key_pages, value_pages, trace)
+    kpool, vpool, kid, vid, prepared = _pair_pools(key_pages, value_pages, trace)
     _record_reads(trace, prepared, "decode_multi_query_step")
-    logits, offsets = _score_tensor(query_slices, pool, kid)
+    logits, offsets = _score_tensor(query_slices, kpool, kid)
     if precomputed_page_logits is not None:
         if len(precomputed_page_logits) != kid.size:
             raise ValueError("precomputed_page_logits must align with key_pages")
@@ -351,14 +353,14 @@ def decode_multi_query_step_hip_tensor(query_slices, key_pages, value_pages, *, 
             if cached is None:
                 continue
             c = torch.as_tensor(np.asarray(cached, dtype=np.float32) if not isinstance(cached, torch.Tensor) else cached,
-                                dtype=torch.float32, device=pool.device)
+                                dtype=torch.float32, device=kpool.device)
             n = int(offsets[i + 1] - offsets[i])
             if c.numel() != n:
                 raise ValueError("precomputed page logits must have shape [token_count]")
             logits[:, offsets[i]: offsets[i + 1]] = c.reshape(1, n)
     weights = logits.clone()
     _softmax_(weights)
-    out = _mix_tensor(weights, pool, vid)
+    out = _mix_tensor(weights, vpool, vid)
     return logits, weights, out
 
 

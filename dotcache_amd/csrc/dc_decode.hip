@@ -292,12 +292,15 @@ int launch_decode_generic(const DecodeArgs& a, hipStream_t stream) {
   return check_hip(hipGetLastError(), "decode_generic_kernel launch");
 }
 
-static int g_decode_path = 0;  // 0 = fastest kernel that fits, 1 = generic kernel only
+// 0 = fastest kernel that fits, 1 = generic kernel only, 2 = MFMA kernel only
+static int g_decode_path = 0;
 
 int launch_decode(const DecodeArgs& a, hipStream_t stream) {
   bool launched = false;
-  if (g_decode_path == 0)
+  if (g_decode_path != 1)
     if (int rc = launch_decode_mfma(a, stream, &launched)) return rc;
+  if (!launched && g_decode_path == 2)
+    return fail(DC_EINVAL, "decode path 2: the MFMA kernel does not cover these pools");
   return launched ? DC_OK : launch_decode_generic(a, stream);
 }
 
@@ -397,7 +400,7 @@ extern "C" int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const
 }
 
 extern "C" int dc_set_decode_path(int32_t path) {
-  if (path != 0 && path != 1) return dc::fail(DC_EINVAL, "decode path must be 0 (auto) or 1 (generic)");
+  if (path < 0 || path > 2) return dc::fail(DC_EINVAL, "decode path must be 0 (auto), 1 (generic) or 2 (mfma)");
   dc::g_decode_path = path;
   return DC_OK;
 }

@@ -83,7 +83,8 @@ __device__ __forceinline__ Split2 split2(float x0, float x1, float neg1) {
 // rarely.
 constexpr float kLazy = 2.f;
 
-// Key-page mix of a pool: only M3 rows, only M0 4-bit codes, or both.
+// Key-page mix of a pool: only M3 rows, only M0 codes (4- or 8-bit, one
+// width per pool), or both.
 enum KeyMode { KEYS_M3 = 0, KEYS_M0 = 1, KEYS_MIXED = 2 };
 
 template <int HD, int VGS, int VBITS>
@@ -113,14 +114,15 @@ struct MfmaCfg {
 // Registers one chunk needs from HBM.  Every chunk issues the same loads
 // whatever its page formats, so the compiler never has to drain the queue to
 // merge register versions.
-template <int HD, int VGS, int VBITS, int KMODE>
+template <int HD, int VGS, int VBITS, int KMODE, int KBITS>
 struct ChunkRegs {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
   static constexpr bool kWordKeys = KMODE == KEYS_M0;
-  // keys: M3 row pieces (8 fp16) or the 16-byte code block of (token, group);
-  // a pool of M0 keys only needs this lane's word of that block
+  static constexpr int KW = KBITS / 4;  // code words of one lane's 8 channels
+  // keys: M3 row pieces (8 fp16) or 16 bytes from this lane's codes of the
+  // (token, group) block; a pool of M0 keys only needs this lane's KW words
   u32x4 kr[kWordKeys ? 1 : 2][kWordKeys ? 1 : Cfg::KG];
-  uint32_t kw[kWordKeys ? 2 : 1][kWordKeys ? Cfg::KG : 1];
+  uint32_t kw[kWordKeys ? 2 : 1][kWordKeys ? Cfg::KG * KW : 1];
   u32x4 vr[Cfg::NVP];  // value code pieces, blob byte order
   uint32_t ks[Cfg::NKS], kbw[Cfg::NKS], vs[Cfg::NVS], vb[Cfg::NVS];  // scale / bias words
 };
@@ -135,12 +137,15 @@ struct PageMeta {
   int c0;                       // first token of the chunk
 };
 
-// KAFF / VAFF: the key / value pool may hold affine M0 pages (bias terms);
-// false drops that code entirely.
-template <int HD, int VGS, int KMODE, int VBITS, bool VM3, bool KAFF, bool VAFF>
+// KBITS: code width of the pool's M0 keys (4 or 8).  KAFF / VAFF: the key /
+// value pool may hold affine M0 pages (bias terms); false drops that code
+// entirely.
+template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF>
 __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
+  static_assert(KBITS == 4 || KBITS == 8, "M0 keys are 4- or 8-bit");
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  using Regs = ChunkRegs<HD, VGS, VBITS, KMODE>;
+  using Regs = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS>;
+  constexpr int KBLK = 4 * KBITS;  // bytes of one (token, group) key code block
   constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W, NACC = Cfg::NACC;
   // two staged chunks in flight where the registers allow it
   constexpr bool kPipe = HD <= 128 && !(VM3 && KMODE == KEYS_MIXED);
@@ -153,8 +158,8 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // bits {0, 1, 3, 4} of t, which puts the 16 rows one read touches in 16
   // distinct bank groups.
   constexpr bool kDmaK = kPipe && KMODE == KEYS_M3 && HD == 128;
-  // pools with M0 keys order each lane's 8 channels as pairs (i, i + 4)
-  constexpr bool kPairedQ = KMODE != KEYS_M3;
+  // pools with 4-bit M0 keys order each lane's 8 channels as pairs (i, i + 4)
+  constexpr bool kPairedQ = KMODE != KEYS_M3 && KBITS == 4;
   __shared__ __attribute__((aligned(16))) uint32_t kbuf0[kDmaK ? 32 * HD / 2 : 1];
   __shared__ __attribute__((aligned(16))) uint32_t kbuf1[kDmaK ? 32 * HD / 2 : 1];
   // key buffer 0 or 1, chosen at compile time (std::integral_constant), so
@@ -269,7 +274,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // k-slot pair i: channels (2i, 2i + 1) of the lane's 8, or (i, i + 4)
-        // where M0 keys occur (the order their nibble unpack produces)
+        // where 4-bit M0 keys occur (the order their nibble unpack produces)
         const int c0 = kPairedQ ? i : 2 * i, c1 = kPairedQ ? i + 4 : 2 * i + 1;
         const float x0 = head_live ? qv[g][c0] * qmul : 0.f, x1 = head_live ? qv[g][c1] * qmul : 0.f;
         qhi[g].u[i] = pack_h2(x0, x1);
@@ -336,9 +341,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   for (int hh = 0; hh < 2; ++hh) {
     const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
     koff_m3[hh] = (ta * HD + 8 * kb) * 2;                     // M3 row piece, channels 8 kb .. of group 0
-    // word kb of the (token, group 0) code block; a 16-byte load from there
-    // (pools with M3 keys too) has that word first and reads on inside the blob
-    koff_m0[hh] = ta * 16 + 4 * kb;
+    // this lane's KW words (channels 8 kb .. 8 kb + 7) of the (token, group
+    // 0) code block; a 16-byte load from there (pools with M3 keys too) has
+    // them first and reads on inside the blob
+    koff_m0[hh] = ta * KBLK + KBITS * kb;
   }
   // key DMA: instruction i writes rows 4 i .. 4 i + 3 of the chunk; lane l
   // takes row 4 i + l / 16, slot l % 16, i.e. source piece (l % 16) ^
@@ -378,17 +384,26 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-          R.kw[hh][g] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(koff_m0[hh]), c0 * 16 + g * CAP * 16, kNT);
+        for (int hh = 0; hh < 2; ++hh) {
+          const int co = c0 * KBLK + g * CAP * KBLK;
+          if constexpr (KBITS == 4) {
+            R.kw[hh][g] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(koff_m0[hh]), co, kNT);
+          } else {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(m.krs, int(koff_m0[hh]), co, kNT);
+            R.kw[hh][2 * g] = x.x;
+            R.kw[hh][2 * g + 1] = x.y;
+          }
+        }
     } else {
       const bool km3 = key_is_m3(m);
-      const int cbase = c0 * (km3 ? HD * 2 : 16);
+      const int cbase = c0 * (km3 ? HD * 2 : KBLK);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const uint32_t lo = km3 ? koff_m3[hh] : koff_m0[hh];
 #pragma unroll
         for (int g = 0; g < KG; ++g) {
-          const int goff = km3 ? 64 * g : g * CAP * 16;
+          const int goff = km3 ? 64 * g : g * CAP * KBLK;
           R.kr[hh][g] = __builtin_amdgcn_raw_buffer_load_b128(m.krs, int(lo), cbase + goff, kNT);
         }
       }
@@ -487,11 +502,11 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = d[i];
         }
       }
-    } else if constexpr (KMODE != KEYS_M3) {  // M0 4-bit, group 32: scale and bias per group in fp32
-      // affine: codes n, bias b; symmetric: codes n - 7, no bias (bf = 0
-      // zeroes the bias words, which then alias the scales)
+    } else if constexpr (KMODE != KEYS_M3) {  // M0 4- or 8-bit, group 32: scale and bias per group in fp32
+      // affine: codes n, bias b; symmetric: codes n - (2^(KBITS-1) - 1), no
+      // bias (bf = 0 zeroes the bias words, which then alias the scales)
       const bool k_affine = KAFF && m.kfmt == DC_FMT_M0_AFFINE;
-      const float zp = k_affine ? 0.f : 7.f;
+      const float zp = k_affine ? 0.f : float((1 << (KBITS - 1)) - 1);
       const float bf = k_affine ? 1.f : 0.f;
       float qb[KG];  // bias weight of group g: sum of the query's group g (affine pages only)
 #pragma unroll
@@ -516,22 +531,30 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         float Lh[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int g = 0; g < KG; ++g) {
-          uint32_t w;
-          if constexpr (Regs::kWordKeys) {
-            w = R.kw[hh][g];
-          } else {
-            w = R.kr[hh][g].x;
-          }
-          // nibble i of the word is channel i; channels i and i + 4 sit 16
-          // bits apart, so one mask and the fp16 magic 0x6400 give the pair
-          // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
-          // (nibbles 1, 3), and one packed add / fma makes it n - zp exactly
           Frag ka;
-          const uint32_t w8 = w >> 8;
-          ka.u[0] = bits_of(h2_of((w & 0x000f000fu) | fp16_magic) + kadd0);
-          ka.u[1] = bits_of(h2_of((w & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
-          ka.u[2] = bits_of(h2_of((w8 & 0x000f000fu) | fp16_magic) + kadd0);
-          ka.u[3] = bits_of(h2_of((w8 & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+          if constexpr (KBITS == 4) {
+            const uint32_t w = Regs::kWordKeys ? R.kw[hh][g] : R.kr[hh][g].x;
+            // nibble i of the word is channel i; channels i and i + 4 sit 16
+            // bits apart, so one mask and the fp16 magic 0x6400 give the pair
+            // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
+            // (nibbles 1, 3), and one packed add / fma makes it n - zp exactly
+            const uint32_t w8 = w >> 8;
+            ka.u[0] = bits_of(h2_of((w & 0x000f000fu) | fp16_magic) + kadd0);
+            ka.u[1] = bits_of(h2_of((w & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+            ka.u[2] = bits_of(h2_of((w8 & 0x000f000fu) | fp16_magic) + kadd0);
+            ka.u[3] = bits_of(h2_of((w8 & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+          } else {
+            // byte i of the two words is channel i: one byte permute puts
+            // bytes (2j, 2j + 1) under the magic's 0x64 bytes, giving the
+            // pair (1024 + n_2j, 1024 + n_2j+1), and one packed add makes
+            // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
+            const uint32_t wa = Regs::kWordKeys ? R.kw[hh][2 * g] : R.kr[hh][g].x;
+            const uint32_t wb = Regs::kWordKeys ? R.kw[hh][2 * g + 1] : R.kr[hh][g].y;
+            ka.u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
+            ka.u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
+            ka.u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
+            ka.u[3] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05030502u)) + kadd0);
+          }
           f32x4 d = {0.f, 0.f, 0.f, 0.f};
           d = mfma(ka, qhi[g], d);
           d = mfma(ka, qlo[g], d);
@@ -589,6 +612,14 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- mix of one staged chunk with its weights ----
+  // The A operand is weight x scale (x 1 for M3 values) times kVS, split
+  // into fp16 high and residual parts.  An 8-bit scale is 17 times finer
+  // than a 4-bit one over the same value range, which puts weight x scale
+  // 2^4 lower in fp16's range, where small products lose bits to
+  // subnormals; kVS = 16 puts it back where 4-bit codes have it (with the
+  // same overflow margin: weight x scale x 16 reaches fp16's maximum only
+  // for 8-bit scales above 1023).  The epilogue divides by kVS.
+  constexpr float kVS = VBITS == 8 ? 16.f : 1.f;
   auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa) __attribute__((always_inline)) {
     bool v_m0 = true;
     if constexpr (VM3) v_m0 = is_m0(m.vfmt);
@@ -596,9 +627,12 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       const bool v_affine = VAFF && m.vfmt == DC_FMT_M0_AFFINE;
       const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
       const float bf = v_affine ? 1.f : 0.f;
-      float pb[8];  // weights of the bias sums (0 on symmetric pages)
+      float pb[8], pw[8];  // weights of the bias sums (0 on symmetric pages), of the codes
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = bf * pa[e];
+      for (int e = 0; e < 8; ++e) {
+        pb[e] = bf * pa[e];
+        pw[e] = kVS * pa[e];
+      }
       // codes become fp16 (1024 + c), or (1024 + 16 c) for a code in the high
       // nibble of its byte; one packed fma maps either to c - zp exactly
       const h2 vadd = VBITS == 4 && (jj & 1) ? h2{(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)}
@@ -621,8 +655,8 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         for (int pp = 0; pp < 4; ++pp) {
           const int e0 = (2 * pp) * VG + g, e1 = (2 * pp + 1) * VG + g;  // (token, group) entries
           // weight x fp16 scale as an fma with a zero addend: one v_fma_mix_f32
-          const float x0 = __builtin_fmaf(pa[2 * pp], float(h2_of(sw[e0 >> 1])[e0 & 1]), 0.f);
-          const float x1 = __builtin_fmaf(pa[2 * pp + 1], float(h2_of(sw[e1 >> 1])[e1 & 1]), 0.f);
+          const float x0 = __builtin_fmaf(pw[2 * pp], float(h2_of(sw[e0 >> 1])[e0 & 1]), 0.f);
+          const float x1 = __builtin_fmaf(pw[2 * pp + 1], float(h2_of(sw[e1 >> 1])[e1 & 1]), 0.f);
           const Split2 sp = split2(x0, x1, neg1);
           fa_hi.u[pp] = sp.hi;
           fa_res.u[pp] = sp.res;
@@ -657,7 +691,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       Frag fa_hi, fa_res;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
-        const Split2 sp = split2(pa[2 * pp], pa[2 * pp + 1], neg1);
+        const Split2 sp = split2(kVS * pa[2 * pp], kVS * pa[2 * pp + 1], neg1);
         fa_hi.u[pp] = sp.hi;
         fa_res.u[pp] = sp.res;
       }
@@ -694,11 +728,11 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     // work instead of per-page scalar work): token count, formats, blob
     // sizes, scale / bias offsets, and its end chunk index in the batch
     // blob layout (dc_common.h blob_layout) of the formats this kernel
-    // accepts, from its fixed geometry: keys M3 fp16 or M0 4-bit group 32,
+    // accepts, from its fixed geometry: keys M3 fp16 or M0 KBITS-bit group 32,
     // values M3 fp16 or M0 VBITS-bit group VGS, capacity CAP
     const int kf = int(k1 >> 16) & 0xff, vf = int(v1 >> 16) & 0xff;
     const uint32_t cap = uint32_t(CAP), m3_bytes = cap * HD * 2;
-    const uint32_t kpay = uint32_t(KG) * cap * 16, ksb = (cap * KG * 2 + 15) & ~15u;
+    const uint32_t kpay = uint32_t(KG) * cap * KBLK, ksb = (cap * KG * 2 + 15) & ~15u;
     const uint32_t vpay = uint32_t(VG) * cap * W * 4, vsb = (cap * VG * 2 + 15) & ~15u;
     const bool km0 = is_m0(kf), vm0 = is_m0(vf), kaff = kf == DC_FMT_M0_AFFINE, vaff = vf == DC_FMT_M0_AFFINE;
     const uint32_t ksc = km0 ? kpay : 0u, kbs = kaff ? kpay + ksb : ksc;
@@ -845,16 +879,17 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
       for (int g = 0; g < VG; ++g)
 #pragma unroll
-        for (int h = 0; h < H; ++h) dq[i * HD + VGS * g + LPW4 * h] = (acc[g * H + h][i] + bq[i][g]) * inv[i];
+        for (int h = 0; h < H; ++h)
+          dq[i * HD + VGS * g + LPW4 * h] = (acc[g * H + h][i] * (1.f / kVS) + bq[i][g]) * inv[i];
   if (!final_out && kb == 0 && head_live) {
     a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 0] = m_ref;
     a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 1] = l;
   }
 }
 
-template <int HD, int VGS, int KMODE, int VBITS, bool VM3, bool KAFF, bool VAFF>
+template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF>
 static int launch_t(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, VBITS, VM3, KAFF, VAFF>), dim3(uint32_t(a.n_items)),
+  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, KBITS, VBITS, VM3, KAFF, VAFF>), dim3(uint32_t(a.n_items)),
                      dim3(64), 0, stream, a);
   return check_hip(hipGetLastError(), "decode_mfma_kernel launch");
 }
@@ -869,35 +904,41 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   if (kg.page_capacity % 32 != 0) return DC_OK;
   // formats present in the pools (bit = format * 9 + bits, as in dc_pool)
   const uint64_t km = a.kpool.format_mask, vm = a.vpool.format_mask;
-  const uint64_t k_m3 = fbit(DC_FMT_M3_F16, 0), k_m0 = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
-  const uint64_t v4 = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
-  const uint64_t v8 = fbit(DC_FMT_M0_AFFINE, 8) | fbit(DC_FMT_M0_SYMMETRIC, 8);
+  const uint64_t m0_4 = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_SYMMETRIC, 4);
+  const uint64_t m0_8 = fbit(DC_FMT_M0_AFFINE, 8) | fbit(DC_FMT_M0_SYMMETRIC, 8);
+  const uint64_t k_m3 = fbit(DC_FMT_M3_F16, 0), k_m0 = m0_4 | m0_8;
   const uint64_t aff = fbit(DC_FMT_M0_AFFINE, 4) | fbit(DC_FMT_M0_AFFINE, 8);
-  if (km == 0 || vm == 0 || (km & ~(k_m3 | k_m0)) || (vm & ~(k_m3 | v4 | v8))) return DC_OK;
-  if ((vm & v4) && (vm & v8)) return DC_OK;  // one value code width per launch
+  if (km == 0 || vm == 0 || (km & ~(k_m3 | k_m0)) || (vm & ~(k_m3 | m0_4 | m0_8))) return DC_OK;
+  // one key code width and one value code width per launch
+  if (((km & m0_4) && (km & m0_8)) || ((vm & m0_4) && (vm & m0_8))) return DC_OK;
   const int kmode = (km & k_m3) && (km & k_m0) ? KEYS_MIXED : (km & k_m3) ? KEYS_M3 : KEYS_M0;
-  const int vbits = (vm & v8) ? 8 : 4;
+  const int kbits = (km & m0_8) ? 8 : 4;
+  const int vbits = (vm & m0_8) ? 8 : 4;
   const bool vm3 = (vm & k_m3) != 0;
   const bool kaff = (km & aff) != 0, vaff = (vm & aff) != 0;
   const int hd = kg.head_dim, vgs = vg.group_size;
   int rc = -1;
   // specialised instantiations for the common pools (every BASELINE
-  // configuration), a general one per shape otherwise
-#define DC_EXACT(HD_, VGS_, KM_, VB_, VM3_, KA_, VA_)                                                    \
-  if (rc < 0 && hd == HD_ && vgs == VGS_ && kmode == KM_ && vbits == VB_ && vm3 == VM3_ && kaff == KA_ && \
-      vaff == VA_)                                                                                       \
-    rc = launch_t<HD_, VGS_, KM_, VB_, VM3_, KA_, VA_>(a, stream);
-#define DC_GENERAL(HD_, VGS_, VB_)                        \
-  if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_) \
-    rc = launch_t<HD_, VGS_, KEYS_MIXED, VB_, true, true, true>(a, stream);
-  DC_EXACT(64, 32, KEYS_M0, 4, false, false, false)     // config 1
-  DC_EXACT(64, 32, KEYS_M0, 4, false, true, true)       // config 2
-  DC_EXACT(128, 32, KEYS_M3, 4, false, false, false)    // config 3
-  DC_EXACT(128, 64, KEYS_MIXED, 8, false, true, false)  // config 4
-  DC_EXACT(128, 64, KEYS_M0, 8, false, true, false)
-  DC_EXACT(128, 32, KEYS_M0, 4, false, true, true)
-  DC_EXACT(256, 32, KEYS_MIXED, 4, true, true, true)  // config 5 (fp16 recent window)
-  DC_EXACT(256, 32, KEYS_M0, 4, false, true, true)
+  // configuration, and 8-bit keys at head_dim 128), a general one per
+  // shape and code widths otherwise (KEYS_M3 ignores kbits)
+#define DC_EXACT(HD_, VGS_, KM_, KB_, VB_, VM3_, KA_, VA_)                                                 \
+  if (rc < 0 && hd == HD_ && vgs == VGS_ && kmode == KM_ && (KM_ == KEYS_M3 || kbits == KB_) &&          \
+      vbits == VB_ && vm3 == VM3_ && kaff == KA_ && vaff == VA_)                                         \
+    rc = launch_t<HD_, VGS_, KM_, KB_, VB_, VM3_, KA_, VA_>(a, stream);
+#define DC_GENERAL(HD_, VGS_, VB_)                                                    \
+  if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_)                             \
+    rc = kbits == 8 ? launch_t<HD_, VGS_, KEYS_MIXED, 8, VB_, true, true, true>(a, stream) \
+                    : launch_t<HD_, VGS_, KEYS_MIXED, 4, VB_, true, true, true>(a, stream);
+  DC_EXACT(64, 32, KEYS_M0, 4, 4, false, false, false)     // config 1
+  DC_EXACT(64, 32, KEYS_M0, 4, 4, false, true, true)       // config 2
+  DC_EXACT(128, 32, KEYS_M3, 4, 4, false, false, false)    // config 3
+  DC_EXACT(128, 64, KEYS_MIXED, 4, 8, false, true, false)  // config 4
+  DC_EXACT(128, 64, KEYS_M0, 4, 8, false, true, false)
+  DC_EXACT(128, 32, KEYS_M0, 4, 4, false, true, true)
+  DC_EXACT(256, 32, KEYS_MIXED, 4, 4, true, true, true)  // config 5 (fp16 recent window)
+  DC_EXACT(256, 32, KEYS_M0, 4, 4, false, true, true)
+  DC_EXACT(128, 32, KEYS_M0, 8, 4, false, true, true)  // 8-bit keys, 4-bit values
+  DC_EXACT(128, 32, KEYS_M0, 8, 8, false, true, true)  // 8-bit keys and values
   DC_GENERAL(64, 32, 4)
   DC_GENERAL(64, 32, 8)
   DC_GENERAL(64, 64, 4)

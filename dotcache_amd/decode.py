@@ -117,11 +117,16 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     return plan
 
 
+_PATHS = {"auto": 0, "generic": 1, "mfma": 2}
+
+
 def set_decode_path(path: str) -> None:
-    """``"auto"`` (MFMA kernel when the pages fit it) or ``"generic"``."""
-    if path not in ("auto", "generic"):
-        raise ValueError("decode path must be 'auto' or 'generic'")
-    _lib.check(_lib.lib().dc_set_decode_path(0 if path == "auto" else 1), "dc_set_decode_path")
+    """``"auto"`` (MFMA kernel when the pages fit it), ``"generic"``, or
+    ``"mfma"`` (the MFMA kernel only: a decode it does not cover raises
+    ValueError)."""
+    if path not in _PATHS:
+        raise ValueError("decode path must be 'auto', 'generic' or 'mfma'")
+    _lib.check(_lib.lib().dc_set_decode_path(_PATHS[path]), "dc_set_decode_path")
 
 
 def workspace_bytes(plan: DecodePlan, n_q: int, head_dim: int) -> int:

@@ -231,12 +231,20 @@ def _gen(shape, gen, dist: str, device):
 
 def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | None = None, batch: int | None = None,
                    context: int | None = None, pages_per_split: int | None = None,
-                   scatter_pages: bool = True) -> Workload:
+                   scatter_pages: bool = True, key_bits: int | None = None) -> Workload:
     """Encode every layer's pages on the device and build its page tables.
     ``layers`` / ``batch`` / ``context`` shrink the workload for tests;
-    ``scatter_pages=False`` keeps each sequence's pages in allocation order."""
+    ``scatter_pages=False`` keeps each sequence's pages in allocation order;
+    ``key_bits`` re-codes the configuration's M0 key pages at that width
+    (a variant named ``<workload>_k<bits>``)."""
     torch = _torch()
     spec = SPECS[name]
+    if key_bits is not None and key_bits != spec.key.bits:
+        from dataclasses import replace
+
+        if spec.key.mode != "M0" or key_bits not in (2, 3, 4, 8):
+            raise ValueError("key_bits re-codes M0 key pages at 2, 3, 4 or 8 bits")
+        spec = replace(spec, name=f"{spec.name}_k{key_bits}", key=replace(spec.key, bits=key_bits))
     if layers is not None or batch is not None or context is not None:
         from dataclasses import replace
 

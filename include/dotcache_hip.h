@@ -232,9 +232,12 @@ int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const void* work
                  int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, int32_t head_dim, float* out, dc_stream_t stream);
 
 /* Process-wide decode kernel choice: 0 (default) runs the MFMA kernel when
- * every page format, head_dim (64/128/256), group size and n_q <= 8 fit it
- * and the generic kernel otherwise; 1 always runs the generic kernel (for
- * cross-checking the two).  Host only; not thread-safe. */
+ * every page format (M3 fp16 keys and values, M0 4- or 8-bit keys of group
+ * 32, M0 4- or 8-bit values of group 32 or 64), head_dim (64/128/256) and
+ * n_q <= 16 fit it, and the generic kernel otherwise; 1 always runs the
+ * generic kernel (for cross-checking the two); 2 runs only the MFMA kernel
+ * and fails with DC_EINVAL where it does not fit (for tests that must know
+ * which kernel ran).  Host only; not thread-safe. */
 int dc_set_decode_path(int32_t path);
 
 #ifdef __cplusplus

@@ -93,3 +93,22 @@ def test_planner_reports_short_tables():
     st = _lib.lib().dc_plan_decode(sp.ctypes.data, 1, 1, 10, C.addressof(items), 2, C.byref(ni), None, 0,
                                    C.byref(nm), C.byref(npart))
     assert st == _lib.DC_ESPACE and ni.value == 10 and nm.value == 1
+
+
+def test_decode_path_switch():
+    """Paths 0 (auto), 1 (generic) and 2 (MFMA only) are accepted; anything
+    else is DC_EINVAL, and the Python wrapper maps names onto them."""
+    from dotcache_amd.decode import set_decode_path
+
+    lib = _lib.lib()
+    try:
+        for path in (0, 1, 2):
+            assert lib.dc_set_decode_path(path) == _lib.DC_OK
+        assert lib.dc_set_decode_path(3) == _lib.DC_EINVAL
+        assert lib.dc_set_decode_path(-1) == _lib.DC_EINVAL
+        for name in ("auto", "generic", "mfma"):
+            set_decode_path(name)
+        with pytest.raises(ValueError):
+            set_decode_path("fast")
+    finally:
+        lib.dc_set_decode_path(0)

@@ -120,24 +120,49 @@ def test_fused_output_only_matches_oracle(kfmt, vfmt, hd, gs, Q):
         assert np.max(np.abs(got - want)) < 2e-4
 
 
-def test_fused_mixed_key_formats_per_page():
-    """Selective key precision: M3 and M0 key pages interleaved in one list."""
+@pytest.mark.parametrize("kbits", [4, 8])
+def test_fused_mixed_key_formats_per_page(kbits):
+    """Selective key precision: M3 and M0 key pages interleaved in one list,
+    on the MFMA kernel."""
     from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
-    from dotcache_amd.types import EncodedPage
+    from dotcache_amd.decode import set_decode_path
 
-    rng = np.random.default_rng(77)
+    set_decode_path("mfma")
+    rng = np.random.default_rng(77 + kbits)
     hd, n = 128, 640
     keys = hard_values(rng, n, hd)
     vals = hard_values(rng, n, hd)
     kp = []
     for i, s in enumerate(range(0, n, 64)):
-        fmt = dict(mode="M3") if i % 3 == 1 else dict(bits=4, scheme="affine")
+        fmt = dict(mode="M3") if i % 3 == 1 else dict(bits=kbits, scheme="affine" if i % 2 else "symmetric")
         kp.append(O.encode_page(keys[s:s + 64], head_dim=hd, group_size=32, kind="K", token_start=s, **fmt))
     vp = _pages(vals, 64, hd, 64, "V", dict(bits=8, scheme="symmetric"))  # V group 64, K group 32 (config 4)
     q = (rng.normal(size=(1, 6, hd)) / np.sqrt(hd)).astype(np.float32)
     want = O.decode_grouped(q, [kp], [vp])
     got = fused(list(q), [[to_product_page(p) for p in kp]], [[to_product_page(p) for p in vp]]).cpu().numpy()
     np.testing.assert_allclose(got, want, atol=2e-4, rtol=0)
+
+
+def test_four_and_eight_bit_keys_in_one_pool_take_the_generic_kernel():
+    """The MFMA kernel takes one key code width per launch: a pool holding
+    both runs on the generic kernel under "auto", and path "mfma" refuses it."""
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+    from dotcache_amd.decode import set_decode_path
+
+    rng = np.random.default_rng(48)
+    hd, n = 128, 320
+    keys = hard_values(rng, n, hd)
+    kp = [O.encode_page(keys[s:s + 64], head_dim=hd, group_size=32, kind="K", token_start=s, bits=4 if i % 2 else 8)
+          for i, s in enumerate(range(0, n, 64))]
+    vp = _pages(hard_values(rng, n, hd), 64, hd, 32, "V", dict(bits=4))
+    q = (rng.normal(size=(1, 4, hd)) / np.sqrt(hd)).astype(np.float32)
+    want = O.decode_grouped(q, [kp], [vp])
+    args = (list(q), [[to_product_page(p) for p in kp]], [[to_product_page(p) for p in vp]])
+    got = fused(*args).cpu().numpy()
+    assert np.max(np.abs(got - want)) < KERNEL_TOL
+    set_decode_path("mfma")
+    with pytest.raises(ValueError, match="MFMA kernel does not cover"):
+        fused(*args)
 
 
 FAST_CASES = [
@@ -149,6 +174,14 @@ FAST_CASES = [
     (dict(bits=4), dict(bits=4), 256, 32, 4, 128),                                 # config 5
     (dict(mode="M3"), dict(mode="M3"), 128, 32, 8, 64),
     (dict(bits=4, scheme="symmetric"), dict(bits=8), 128, 32, 5, 96),
+    # 8-bit keys: specialised instances at head_dim 128, group 32 values
+    (dict(bits=8), dict(bits=4), 128, 32, 6, 64),
+    (dict(bits=8), dict(bits=8), 128, 32, 8, 64),
+    # and the general instances (symmetric keys, other shapes)
+    (dict(bits=8, scheme="symmetric"), dict(bits=8, scheme="symmetric"), 128, 32, 4, 64),
+    (dict(bits=8), dict(bits=8, scheme="symmetric"), 128, 64, 6, 64),
+    (dict(bits=8), dict(bits=4, scheme="symmetric"), 64, 32, 3, 64),
+    (dict(bits=8, scheme="symmetric"), dict(bits=4), 256, 32, 4, 128),
 ]
 
 
@@ -159,11 +192,13 @@ FAST_CASES = [
 KERNEL_TOL = 3e-4
 
 
-@pytest.mark.parametrize("path", ["auto", "generic"])
+@pytest.mark.parametrize("path", ["mfma", "generic"])
 @pytest.mark.parametrize("kfmt,vfmt,hd,vgs,Q,tpp", FAST_CASES)
 def test_fused_kernels_match_oracle(kfmt, vfmt, hd, vgs, Q, tpp, path):
-    """The MFMA kernel (auto) and the generic kernel on the same pages, with
-    ragged groups, partial last pages, outlier channels and split-K."""
+    """The MFMA kernel and the generic kernel on the same pages, with ragged
+    groups, partial last pages, outlier channels and split-K.  Path "mfma"
+    raises if the MFMA kernel does not take the call, so every case here is
+    shown to run on it."""
     from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
     from dotcache_amd.decode import set_decode_path
 
@@ -245,7 +280,7 @@ def test_lse_merge_matches_float64(hd):
         np.testing.assert_allclose(got[s, h], want, atol=2e-5, rtol=2e-5)
 
 
-@pytest.mark.parametrize("path", ["auto", "generic"])
+@pytest.mark.parametrize("path", ["mfma", "generic"])
 @pytest.mark.parametrize("kfmt,vfmt,vgs", [
     (dict(mode="M3"), dict(bits=4, scheme="symmetric"), 32),   # config 3 formats (keys through LDS)
     (dict(bits=4), dict(bits=8, scheme="symmetric"), 64),      # config 4 formats
