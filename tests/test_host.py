@@ -54,3 +54,14 @@ def test_split_policy_fills_the_chip():
     per = choose_pages_per_split(np.full(8, 256), 4)
     assert per >= 8 and 8 * 4 * (-(-256 // per)) >= 256
     assert choose_pages_per_split(np.array([1]), 1) == 1
+
+
+def test_workload_key_bits_variant_is_validated_before_any_device_work():
+    """``key_bits`` re-codes M0 key pages only: configurations whose keys are
+    M3 rows, and widths the encoder does not have, are refused up front."""
+    from dotcache_amd.workloads import build_workload
+
+    with pytest.raises(ValueError, match="M0 key pages"):
+        build_workload("c3", key_bits=8, device="cpu")
+    with pytest.raises(ValueError, match="M0 key pages"):
+        build_workload("c2", key_bits=5, device="cpu")
