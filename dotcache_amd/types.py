@@ -68,6 +68,12 @@ class EncodedPage:
     bias: np.ndarray | None = None
     escape_payload: np.ndarray | None = None
     escape_scales: np.ndarray | None = None
+    # shortlist metadata of the raw rows (fp16), as the reference encoder
+    # stores it (encode.py:64-75); None where the page was built without it
+    runtime_page_mean: np.ndarray | None = None
+    runtime_page_sketch: np.ndarray | None = None
+    runtime_page_min: np.ndarray | None = None
+    runtime_page_max: np.ndarray | None = None
     requested_mode: str | None = None
     full_page_decode_calls: int = 0
     decode_group_calls: int = 0

@@ -178,6 +178,32 @@ int dc_mix_pages(dc_pool pool, const int32_t* page_ids, const int32_t* token_off
  * point that returns logits and weights. */
 int dc_softmax_rows(float* x /* device */, int32_t n_rows, int32_t n_cols, int64_t stride, dc_stream_t stream);
 
+/* Execution shortlist (reference dotcache/session_runtime.py:122-439).
+ *
+ * Per-page summaries of pages page_ids[0 .. n_pages) of a pool, from their
+ * dequantised rows: mean [n][head_dim], sketch [n][sketch_rows][head_dim]
+ * (means of np.array_split(rows, min(sketch_rows, tokens)); rows past that
+ * repeat the last chunk mean), page_min / page_max [n][head_dim].  Replaces
+ * the dense fallbacks of sketch_key_page / summarize_value_page /
+ * envelope_key_page (session_runtime.py:122-162), which decode the page on
+ * the host.  head_dim <= 256. */
+int dc_page_summaries(dc_pool pool, const int32_t* page_ids, int32_t n_pages, int32_t sketch_rows, float* mean,
+                      float* sketch, float* page_min, float* page_max, dc_stream_t stream);
+
+/* scores[p] = max_s sketch[p, s, :] . query (mode 0, "sketch") or
+ * page_max[p, :] . max(query, 0) + page_min[p, :] . min(query, 0) (mode 1,
+ * "envelope").  Replaces score_page_relevance and the candidate scoring of
+ * select_execution_page_indices (session_runtime.py:165-186, :268-423). */
+int dc_page_relevance(const float* sketch, int32_t sketch_rows, const float* page_min, const float* page_max,
+                      int32_t mode, const float* query, int32_t head_dim, int32_t n_pages, float* scores,
+                      dc_stream_t stream);
+
+/* selected[i] = 1 for the k best candidates (candidate[i] != 0) by score,
+ * descending, ties to the lower index; 0 elsewhere.  Replaces the ranking
+ * of select_execution_page_indices (session_runtime.py:425-436). */
+int dc_select_top_k(const float* scores, const uint8_t* candidate, int32_t n, int32_t k, uint8_t* selected,
+                    dc_stream_t stream);
+
 /* ---- read path: fused paged decode ------------------------------------ */
 
 /* Host-only planner: split each (sequence, kv_head)'s page list into

@@ -292,6 +292,10 @@ class OraclePage:
     bias: np.ndarray | None = None
     escape_payload: np.ndarray | None = None
     escape_scales: np.ndarray | None = None
+    runtime_page_mean: np.ndarray | None = None
+    runtime_page_sketch: np.ndarray | None = None
+    runtime_page_min: np.ndarray | None = None
+    runtime_page_max: np.ndarray | None = None
     full_page_decode_calls: int = 0
     extra: dict = field(default_factory=dict)
 
@@ -323,6 +327,7 @@ def encode_page(
     sensitivity_tier: str = "exact",
     fallback_reason: str = "",
     age_bucket: str = "aged",
+    build_runtime_metadata: bool = False,
 ) -> OraclePage:
     """Encode ``values [T, head_dim]`` into one page.
 
@@ -347,10 +352,11 @@ def encode_page(
         quant_scheme=scheme, policy_id=policy_id, sensitivity_tier=sensitivity_tier,
         fallback_reason=fallback_reason, age_bucket=age_bucket,
     )
+    runtime = runtime_page_metadata(x) if build_runtime_metadata and x.shape[0] > 0 else {}
     if mode == "M3":
         header = OracleHeader(padded_head_dim=ng * group_size, mode_default="M3", escape_dtype=escape_dtype, **common)
         esc, esc_scales = encode_escape_storage(x, dtype=escape_dtype)
-        return OraclePage(header=header, escape_payload=esc, escape_scales=esc_scales)
+        return OraclePage(header=header, escape_payload=esc, escape_scales=esc_scales, **runtime)
     if mode != "M0":
         raise ValueError("only M0 and M3 pages are on this path")
     codes, scales, bias, phd = quantize_tensor(x, group_size=group_size, bits=bits, scheme=scheme)
@@ -360,6 +366,26 @@ def encode_page(
         payload=build_payload(codes, bits, layout),
         scales=scales.astype(np.float16),
         bias=None if bias is None else bias.astype(np.float16),
+        **runtime,
+    )
+
+
+RUNTIME_SKETCH_ROWS = 4  # reference encode.py:17
+
+
+def runtime_page_metadata(values) -> dict:
+    """The shortlist metadata the reference encoder stores with a page, from
+    the raw (unquantised) rows: fp16 mean, fp16 means of
+    ``np.array_split(rows, min(4, T))``, fp16 per-channel min and max --
+    reference ``encode.py:64-75`` (built at ``:163-165``)."""
+    x = np.asarray(values, dtype=np.float32)
+    rows = min(max(1, RUNTIME_SKETCH_ROWS), x.shape[0])
+    chunks = np.array_split(x, rows, axis=0)
+    return dict(
+        runtime_page_mean=x.mean(axis=0).astype(np.float16),
+        runtime_page_sketch=np.stack([c.mean(axis=0) for c in chunks], axis=0).astype(np.float16),
+        runtime_page_min=x.min(axis=0).astype(np.float16),
+        runtime_page_max=x.max(axis=0).astype(np.float16),
     )
 
 

@@ -10,6 +10,8 @@ def to_product_page(op) -> EncodedPage:
         header=PageHeader.from_dict(op.header.to_dict()),
         payload=op.payload, scales=op.scales, bias=op.bias,
         escape_payload=op.escape_payload, escape_scales=op.escape_scales,
+        runtime_page_mean=op.runtime_page_mean, runtime_page_sketch=op.runtime_page_sketch,
+        runtime_page_min=op.runtime_page_min, runtime_page_max=op.runtime_page_max,
     )
 
 

@@ -40,14 +40,16 @@ def test_window_indices_known_answers(recent, sink, want):
         assert select_window_page_indices(kp, recent_window_tokens=recent, sink_window_tokens=sink) == want
 
 
-def test_shortlist_requests_are_refused():
+def test_shortlist_argument_checks():
+    """The reference's errors: a shortlist needs a query, the mode must be
+    sketch or envelope, the sketch size positive, key and value lists equal."""
     kp = _paged(128, 4, "K")
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="query_slice"):
         select_execution_page_indices(kp, relevance_top_k=1)
-    with pytest.raises(ValueError):
-        PagedDecodeSession(relevance_top_k=2)
-    with pytest.raises(ValueError):
-        PagedDecodeSession(approximate_old_pages=True)
+    with pytest.raises(ValueError, match="relevance_mode"):
+        PagedDecodeSession(relevance_top_k=2, relevance_mode="dense")
+    with pytest.raises(ValueError, match="sketch_size"):
+        PagedDecodeSession(relevance_top_k=2, relevance_sketch_size=0)
     with pytest.raises(ValueError):
         select_execution_page_pairs(kp, kp[:1])
 
