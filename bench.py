@@ -49,6 +49,9 @@ def parse():
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from Python each step instead of replaying captured HIP graphs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--shortlist-pages", type=int, default=0, metavar="N",
+                    help="only time the execution shortlist kernels: relevance of N pages (4-row sketches, "
+                         "head_dim 128) and the top-k of one 2048-page stream; prints its own JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy a BYTES-sized device buffer three times and exit: the known-size "
@@ -69,6 +72,58 @@ def profiled_traffic(workload: str, pages_per_split: int, decode_path: str):
                     workload, pages_per_split, decode_path):
                 return float(rec["traffic_bytes"])
     return None
+
+
+def shortlist_probe(n_pages: int, steps: int) -> None:
+    """Time dc_page_relevance over n_pages 4-row fp32 sketches (an HBM-bound
+    GEMV: 4 x 128 x 4 bytes per page) and dc_select_top_k over one stream of
+    2048 pages (k = 64), each replayed ``steps`` times between events."""
+    import ctypes as C
+
+    import torch
+
+    from dotcache_amd import _lib
+    from dotcache_amd.page_pool import current_stream_ptr
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    S, hd, n_tk, k = 4, 128, 2048, 64
+    sk = torch.randn((n_pages, S, hd), device=dev, generator=g)
+    lo = torch.randn((n_pages, hd), device=dev, generator=g)
+    hi = lo + 1.0
+    q = torch.randn(hd, device=dev, generator=g)
+    scores = torch.empty(n_pages, device=dev)
+    cand = torch.ones(n_tk, dtype=torch.uint8, device=dev)
+    sel = torch.empty(n_tk, dtype=torch.uint8, device=dev)
+    L = _lib.lib()
+    stream = C.c_void_p(current_stream_ptr())
+
+    def relevance():
+        _lib.check(L.dc_page_relevance(C.c_void_p(sk.data_ptr()), S, C.c_void_p(lo.data_ptr()), C.c_void_p(hi.data_ptr()),
+                                       0, C.c_void_p(q.data_ptr()), hd, n_pages, C.c_void_p(scores.data_ptr()), stream),
+                   "dc_page_relevance")
+
+    def topk():
+        _lib.check(L.dc_select_top_k(C.c_void_p(scores.data_ptr()), C.c_void_p(cand.data_ptr()), n_tk, k,
+                                     C.c_void_p(sel.data_ptr()), stream), "dc_select_top_k")
+
+    out = {}
+    for name, fn in (("relevance", relevance), ("top_k", topk)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        out[name] = a.elapsed_time(b) * 1e3 / steps
+    nbytes = n_pages * S * hd * 4
+    print(json.dumps({"metric": "execution shortlist: pages scored/s", "value": n_pages / (out["relevance"] * 1e-6),
+                      "unit": "pages/s", "relevance_us": out["relevance"], "relevance_bytes": nbytes,
+                      "relevance_hbm_frac": nbytes / (out["relevance"] * 1e-6) / (HBM_PEAK_GBPS * 1e9),
+                      "top_k_us": out["top_k"], "top_k_pages": n_tk, "k": k, "steps": steps}), flush=True)
 
 
 def copy_probe(nbytes: int) -> None:
@@ -149,6 +204,9 @@ def main():
 
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.shortlist_pages:
+        shortlist_probe(args.shortlist_pages, max(args.steps, 1))
         return
 
     from dotcache_amd.decode import set_decode_path

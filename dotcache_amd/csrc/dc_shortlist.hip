@@ -100,27 +100,38 @@ __global__ void __launch_bounds__(256) page_relevance_kernel(const float* __rest
 
 // Stable top-k among candidates: page i is taken when fewer than k
 // candidates rank before it, ranking by score descending and, among equal
-// scores, by index ascending (Python's stable sort with reverse=True).
-// Scores of other blocks are staged through LDS 256 at a time.
-__global__ void __launch_bounds__(256) select_top_k_kernel(const float* __restrict__ scores,
-                                                           const uint8_t* __restrict__ candidate, int32_t n,
-                                                           int32_t k, uint8_t* selected) {
-  __shared__ float s_sc[256];
-  __shared__ uint8_t s_cand[256];
-  const int i = blockIdx.x * 256 + threadIdx.x;
+// scores, by index ascending (Python's stable sort with reverse=True).  One
+// wave per 64 pages; the scores go through LDS a tile of kTopKTile at a time,
+// non-candidates as -inf (which never rank before a finite score; an equal
+// score counts only for a candidate), read four at a time.
+constexpr int kTopKTile = 4096;
+__global__ void __launch_bounds__(64) select_top_k_kernel(const float* __restrict__ scores,
+                                                          const uint8_t* __restrict__ candidate, int32_t n,
+                                                          int32_t k, uint8_t* selected) {
+  __shared__ __attribute__((aligned(16))) float s_sc[kTopKTile];
+  __shared__ __attribute__((aligned(16))) float s_ok[kTopKTile];
+  const int i = blockIdx.x * 64 + threadIdx.x;
   const bool mine = i < n && candidate[i] != 0;
   const float si = i < n ? scores[i] : 0.f;
   int rank = 0;
-  for (int base = 0; base < n; base += 256) {
-    const int j = base + threadIdx.x;
-    s_sc[threadIdx.x] = j < n ? scores[j] : 0.f;
-    s_cand[threadIdx.x] = j < n ? candidate[j] : 0;
+  for (int base = 0; base < n; base += kTopKTile) {
+    const int m = n - base < kTopKTile ? n - base : kTopKTile;
+    const int m4 = (m + 3) & ~3;
+    for (int u = threadIdx.x; u < m4; u += 64) {
+      const bool in = u < m && candidate[base + u] != 0;
+      s_sc[u] = in ? scores[base + u] : -INFINITY;
+      s_ok[u] = in ? 1.f : 0.f;
+    }
     __syncthreads();
     if (mine) {
-      const int m = n - base < 256 ? n - base : 256;
-      for (int u = 0; u < m; ++u) {
-        const float sj = s_sc[u];
-        rank += (s_cand[u] != 0) && (sj > si || (sj == si && base + u < i));
+      for (int u = 0; u < m4; u += 4) {
+        const float4 sj = *reinterpret_cast<const float4*>(s_sc + u);
+        const float4 ok = *reinterpret_cast<const float4*>(s_ok + u);
+        const int j = base + u;
+        rank += (sj.x > si) | ((sj.x == si) & (ok.x != 0.f) & (j < i));
+        rank += (sj.y > si) | ((sj.y == si) & (ok.y != 0.f) & (j + 1 < i));
+        rank += (sj.z > si) | ((sj.z == si) & (ok.z != 0.f) & (j + 2 < i));
+        rank += (sj.w > si) | ((sj.w == si) & (ok.w != 0.f) & (j + 3 < i));
       }
     }
     __syncthreads();
@@ -161,7 +172,7 @@ extern "C" int dc_select_top_k(const float* scores, const uint8_t* candidate, in
   if (n < 0 || k < 0) return dc::fail(DC_EINVAL, "dc_select_top_k: n and k must be non-negative");
   if (n == 0) return DC_OK;
   if (!scores || !candidate || !selected) return dc::fail(DC_EINVAL, "dc_select_top_k: null pointer");
-  hipLaunchKernelGGL(dc::select_top_k_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, hipStream_t(stream),
+  hipLaunchKernelGGL(dc::select_top_k_kernel, dim3(uint32_t((n + 63) / 64)), dim3(64), 0, hipStream_t(stream),
                      scores, candidate, n, k, selected);
   return dc::check_hip(hipGetLastError(), "dc_select_top_k launch");
 }
