@@ -88,12 +88,17 @@ def encode_page(
     page_mode: PageModeSpec | None = None,
     layout: str | None = None,
     quant_scheme: str | None = None,
+    build_runtime_metadata: bool = True,
     device="cuda",
 ) -> EncodedPage:
     """Reference ``encode_page`` computed by the HIP encoder.
 
     ``tensor_slice`` is ``[token_count, head_dim]`` (numpy or torch; it is
     read as fp32, or as its own fp16/bf16 dtype when it is a torch tensor).
+    With ``build_runtime_metadata`` (the reference's default) the page also
+    carries the shortlist metadata of its raw rows, computed with numpy as
+    the reference computes it (``encode.py:64-75``): fp16 mean, fp16 means
+    of ``np.array_split(rows, min(4, T))``, fp16 min and max.
     """
     torch = _torch()
     if isinstance(tensor_slice, torch.Tensor):
@@ -122,4 +127,11 @@ def encode_page(
     finally:
         pool.free(pid)
     page.requested_mode = spec["mode"]
+    if build_runtime_metadata and T:
+        x = values.float().cpu().numpy()
+        chunks = np.array_split(x, min(4, T), axis=0)
+        page.runtime_page_mean = x.mean(axis=0).astype(np.float16)
+        page.runtime_page_sketch = np.stack([c.mean(axis=0) for c in chunks], axis=0).astype(np.float16)
+        page.runtime_page_min = x.min(axis=0).astype(np.float16)
+        page.runtime_page_max = x.max(axis=0).astype(np.float16)
     return page
