@@ -335,7 +335,8 @@ def encode_page(
     of presentation only: the config / page-mode resolution of ``:144-155``
     is done by the caller, who passes the resolved ``bits``, ``mode``,
     ``scheme`` and ``layout``; the runtime sketch/envelope metadata of
-    ``:163-165`` (shortlist-only, not read by score or mix) is not built.
+    ``:163-165`` (shortlist-only, not read by score or mix) is built only
+    with ``build_runtime_metadata=True`` (:func:`runtime_page_metadata`).
     M0 scales and biases are stored as fp16 (``:427-428``); the codes are
     computed with the fp32 scale before that rounding (``m0_affine.py``).
     """

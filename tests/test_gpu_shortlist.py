@@ -155,3 +155,23 @@ def test_session_decode_with_shortlist_matches_the_oracle(cfg, meta):
     assert 2 < len(want_idx) < len(kp)
     for a, b, name in zip(got, want, ("logits", "weights", "output")):
         np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-4, err_msg=name)
+
+
+def test_encode_page_stores_the_reference_runtime_metadata():
+    """``encode_page`` (device encoder) carries the fp16 mean, 4-row chunk
+    sketch, min and max of the raw rows, equal to the oracle's numpy
+    restatement of reference ``encode.py:64-75``; a 3-token page has 3 rows."""
+    from dotcache_amd.config import DotCacheConfig
+    from dotcache_amd.encode import encode_page
+
+    rng = np.random.default_rng(19)
+    cfg = DotCacheConfig(head_dim=32, group_size=32, bits_k=4, tokens_per_page=64)
+    for t in (64, 50, 3):
+        x = rng.normal(size=(t, 32)).astype(np.float32)
+        page = encode_page(x, cfg, kind="K")
+        want = O.runtime_page_metadata(x)
+        for name, arr in want.items():
+            np.testing.assert_array_equal(getattr(page, name), arr, err_msg=f"{name} T={t}")
+        assert page.runtime_page_sketch.shape == (min(4, t), 32)
+    bare = encode_page(x, cfg, kind="K", build_runtime_metadata=False)
+    assert bare.runtime_page_sketch is None and bare.runtime_page_mean is None
