@@ -100,31 +100,37 @@ __global__ void __launch_bounds__(256) page_relevance_kernel(const float* __rest
 
 // Stable top-k among candidates: page i is taken when fewer than k
 // candidates rank before it, ranking by score descending and, among equal
-// scores, by index ascending (Python's stable sort with reverse=True).  One
-// wave per 64 pages; the scores go through LDS a tile of kTopKTile at a time,
-// non-candidates as -inf (which never rank before a finite score; an equal
-// score counts only for a candidate), read four at a time.
+// scores, by index ascending (Python's stable sort with reverse=True).  A
+// block of four waves ranks 64 pages: lane l of every wave takes page
+// 64 blockIdx + l and wave w counts over a quarter of each tile, the four
+// partial counts meeting in LDS.  The scores go through LDS a tile of
+// kTopKTile at a time, non-candidates as -inf (which never rank before a
+// finite score; an equal score counts only for a candidate), read four at a
+// time.
 constexpr int kTopKTile = 4096;
-__global__ void __launch_bounds__(64) select_top_k_kernel(const float* __restrict__ scores,
-                                                          const uint8_t* __restrict__ candidate, int32_t n,
-                                                          int32_t k, uint8_t* selected) {
+__global__ void __launch_bounds__(256) select_top_k_kernel(const float* __restrict__ scores,
+                                                           const uint8_t* __restrict__ candidate, int32_t n,
+                                                           int32_t k, uint8_t* selected) {
   __shared__ __attribute__((aligned(16))) float s_sc[kTopKTile];
   __shared__ __attribute__((aligned(16))) float s_ok[kTopKTile];
-  const int i = blockIdx.x * 64 + threadIdx.x;
+  __shared__ int s_rank[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = blockIdx.x * 64 + lane;
   const bool mine = i < n && candidate[i] != 0;
   const float si = i < n ? scores[i] : 0.f;
   int rank = 0;
   for (int base = 0; base < n; base += kTopKTile) {
     const int m = n - base < kTopKTile ? n - base : kTopKTile;
-    const int m4 = (m + 3) & ~3;
-    for (int u = threadIdx.x; u < m4; u += 64) {
+    const int m16 = (m + 15) & ~15;  // <= kTopKTile, a multiple of 16: four quarters of whole float4s
+    for (int u = threadIdx.x; u < m16; u += 256) {
       const bool in = u < m && candidate[base + u] != 0;
       s_sc[u] = in ? scores[base + u] : -INFINITY;
       s_ok[u] = in ? 1.f : 0.f;
     }
     __syncthreads();
     if (mine) {
-      for (int u = 0; u < m4; u += 4) {
+      const int q = m16 / 4;
+      for (int u = w * q; u < (w + 1) * q; u += 4) {
         const float4 sj = *reinterpret_cast<const float4*>(s_sc + u);
         const float4 ok = *reinterpret_cast<const float4*>(s_ok + u);
         const int j = base + u;
@@ -136,7 +142,12 @@ __global__ void __launch_bounds__(64) select_top_k_kernel(const float* __restric
     }
     __syncthreads();
   }
-  if (i < n) selected[i] = mine && rank < k ? 1 : 0;
+  s_rank[w][lane] = rank;
+  __syncthreads();
+  if (w == 0 && i < n) {
+    const int total = s_rank[0][lane] + s_rank[1][lane] + s_rank[2][lane] + s_rank[3][lane];
+    selected[i] = mine && total < k ? 1 : 0;
+  }
 }
 
 }  // namespace dc
@@ -172,7 +183,7 @@ extern "C" int dc_select_top_k(const float* scores, const uint8_t* candidate, in
   if (n < 0 || k < 0) return dc::fail(DC_EINVAL, "dc_select_top_k: n and k must be non-negative");
   if (n == 0) return DC_OK;
   if (!scores || !candidate || !selected) return dc::fail(DC_EINVAL, "dc_select_top_k: null pointer");
-  hipLaunchKernelGGL(dc::select_top_k_kernel, dim3(uint32_t((n + 63) / 64)), dim3(64), 0, hipStream_t(stream),
+  hipLaunchKernelGGL(dc::select_top_k_kernel, dim3(uint32_t((n + 63) / 64)), dim3(256), 0, hipStream_t(stream),
                      scores, candidate, n, k, selected);
   return dc::check_hip(hipGetLastError(), "dc_select_top_k launch");
 }
