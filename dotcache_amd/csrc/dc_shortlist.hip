@@ -65,37 +65,39 @@ __global__ void __launch_bounds__(256) page_summaries_kernel(dc_pool pool, const
   pmax[int64_t(p) * hd + c] = hi;
 }
 
-// One wave per page: sketch mode, max over rows s of sketch[p, s, :] . q;
-// envelope mode, max[p, :] . max(q, 0) + min[p, :] . min(q, 0).
+// One wave per page, the waves striding over the pages (a launch of at most
+// 8192 waves, each scoring n / 8192 pages in turn): sketch mode, max over
+// rows s of sketch[p, s, :] . q; envelope mode, max[p, :] . max(q, 0) +
+// min[p, :] . min(q, 0).
 __global__ void __launch_bounds__(256) page_relevance_kernel(const float* __restrict__ sketch, int32_t sketch_rows,
                                                              const float* __restrict__ pmin,
                                                              const float* __restrict__ pmax, int32_t mode,
                                                              const float* __restrict__ query, int32_t hd,
                                                              int32_t n_pages, float* scores) {
   const int lane = threadIdx.x & 63;
-  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (p >= n_pages) return;
-  float best = -INFINITY;
-  if (mode == 0) {
-    for (int s = 0; s < sketch_rows; ++s) {
-      const float* row = sketch + (int64_t(p) * sketch_rows + s) * hd;
+  for (int p = blockIdx.x * 4 + (threadIdx.x >> 6); p < n_pages; p += gridDim.x * 4) {
+    float best = -INFINITY;
+    if (mode == 0) {
+      for (int s = 0; s < sketch_rows; ++s) {
+        const float* row = sketch + (int64_t(p) * sketch_rows + s) * hd;
+        float acc = 0.f;
+        for (int c = lane; c < hd; c += 64) acc += row[c] * query[c];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        best = fmaxf(best, acc);
+      }
+    } else {
       float acc = 0.f;
-      for (int c = lane; c < hd; c += 64) acc += row[c] * query[c];
+      for (int c = lane; c < hd; c += 64) {
+        const float qc = query[c];
+        acc += pmax[int64_t(p) * hd + c] * fmaxf(qc, 0.f) + pmin[int64_t(p) * hd + c] * fminf(qc, 0.f);
+      }
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-      best = fmaxf(best, acc);
+      best = acc;
     }
-  } else {
-    float acc = 0.f;
-    for (int c = lane; c < hd; c += 64) {
-      const float qc = query[c];
-      acc += pmax[int64_t(p) * hd + c] * fmaxf(qc, 0.f) + pmin[int64_t(p) * hd + c] * fminf(qc, 0.f);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    best = acc;
+    if (lane == 0) scores[p] = best;
   }
-  if (lane == 0) scores[p] = best;
 }
 
 // Stable top-k among candidates: page i is taken when fewer than k
@@ -173,7 +175,8 @@ extern "C" int dc_page_relevance(const float* sketch, int32_t sketch_rows, const
   if (n_pages == 0) return DC_OK;
   if (!query || !scores || (mode == 0 && !sketch) || (mode == 1 && (!page_min || !page_max)))
     return dc::fail(DC_EINVAL, "dc_page_relevance: null pointer");
-  hipLaunchKernelGGL(dc::page_relevance_kernel, dim3(uint32_t((n_pages + 3) / 4)), dim3(256), 0, hipStream_t(stream),
+  const uint32_t blocks = uint32_t((n_pages + 3) / 4 < 2048 ? (n_pages + 3) / 4 : 2048);
+  hipLaunchKernelGGL(dc::page_relevance_kernel, dim3(blocks), dim3(256), 0, hipStream_t(stream),
                      sketch, sketch_rows, page_min, page_max, mode, query, head_dim, n_pages, scores);
   return dc::check_hip(hipGetLastError(), "dc_page_relevance launch");
 }
