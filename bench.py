@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--shortlist-pages", type=int, default=0, metavar="N",
                     help="only time the execution shortlist kernels: relevance of N pages (4-row sketches, "
-                         "head_dim 128) and the top-k of one 2048-page stream; prints its own JSON line")
+                         "head_dim 128) and the top-k of one min(N, 2048)-page stream; prints its own JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy a BYTES-sized device buffer three times and exit: the known-size "
@@ -77,7 +77,8 @@ def profiled_traffic(workload: str, pages_per_split: int, decode_path: str):
 def shortlist_probe(n_pages: int, steps: int) -> None:
     """Time dc_page_relevance over n_pages 4-row fp32 sketches (an HBM-bound
     GEMV: 4 x 128 x 4 bytes per page) and dc_select_top_k over one stream of
-    2048 pages (k = 64), each replayed ``steps`` times between events."""
+    min(n_pages, 2048) pages (k = 64), each replayed ``steps`` times between
+    events."""
     import ctypes as C
 
     import torch
@@ -87,7 +88,9 @@ def shortlist_probe(n_pages: int, steps: int) -> None:
 
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev).manual_seed(0)
-    S, hd, n_tk, k = 4, 128, 2048, 64
+    # the top-k ranks the first n_tk of the relevance scores: never more than exist
+    S, hd, k = 4, 128, 64
+    n_tk = min(2048, n_pages)
     sk = torch.randn((n_pages, S, hd), device=dev, generator=g)
     lo = torch.randn((n_pages, hd), device=dev, generator=g)
     hi = lo + 1.0
@@ -137,15 +140,26 @@ def copy_probe(nbytes: int) -> None:
     log(f"copied {nbytes} bytes x3")
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(wl, budget_s: float) -> dict:
     """Time the CPU oracle (numpy restatement of the reference cpu_ref path:
     per page score, one global softmax, per page mix, one query head at a
-    time) on a bounded sample of the same workload: layer 0, (sequence, KV
-    head) streams in order, every GQA query head of each, until
-    ``budget_s`` of CPU time is spent.  One (sequence, layer, token)
-    position covers all KV heads, so the rate is tokens of the streams done
-    / KV heads / seconds (the per-token cost is linear in the context, so
-    the sample extrapolates per token position)."""
+    time) on a bounded sample of the same workload: layer 0's (sequence, KV
+    head) streams in order, every GQA query head of each.  Two slices of the
+    same streams check that the cost per token position is linear in the
+    context: first each stream cut to half its pages (a third of the
+    budget), then the whole streams (the rest).  One (sequence, layer,
+    token) position covers all KV heads, so a rate is tokens done / KV heads
+    / seconds; ``value`` is the whole-stream slice's."""
     from threadpoolctl import threadpool_limits
 
     from oracle import dotcache_oracle as O
@@ -161,36 +175,45 @@ def cpu_baseline(wl, budget_s: float) -> dict:
         return O.OraclePage(header=oh, payload=page.payload, scales=page.scales, bias=page.bias,
                             escape_payload=page.escape_payload, escape_scales=page.escape_scales)
 
-    tokens = 0
-    streams = 0
-    dt = 0.0
-    with threadpool_limits(limits=1):
+    def run(fraction: float, budget: float):
+        tokens = streams = 0
+        dt = 0.0
         for b in range(spec.batch):
             n = int(lt.seq_pages[b])
+            keep = max(1, int(round(n * fraction)))
             kt = lt.k_table[b].cpu().numpy()
             vt = lt.v_table[b].cpu().numpy()
             for h in range(H):
-                kp = [to_oracle(wl.k_pool, kt[h, p], "K") for p in range(n)]
-                vp = [to_oracle(wl.v_pool, vt[h, p], "V") for p in range(n)]
+                kp = [to_oracle(wl.k_pool, kt[h, p], "K") for p in range(keep)]
+                vp = [to_oracle(wl.v_pool, vt[h, p], "V") for p in range(keep)]
                 t0 = time.perf_counter()
                 for j in range(Q):
                     O.decode_step(q_all[b, h, j], kp, vp)
                 dt += time.perf_counter() - t0
                 tokens += sum(p.header.token_count for p in kp)
                 streams += 1
-                if dt > budget_s:
-                    break
-            if dt > budget_s:
-                break
+                if dt > budget:
+                    return tokens, streams, dt
+        return tokens, streams, dt
+
+    with threadpool_limits(limits=1):
+        t_half, s_half, dt_half = run(0.5, budget_s / 3)
+        tokens, streams, dt = run(1.0, budget_s * 2 / 3)
     rate = tokens / H / dt
+    rate_half = t_half / H / dt_half
     return {
         "value": rate,
         "unit": "KV tokens/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"layer 0: {streams} (sequence, KV head) streams x {Q} query heads, {tokens} tokens, "
-                  f"{dt:.1f} s of oracle time (page downloads excluded); numpy oracle of reference cpu_ref, "
-                  f"BLAS pinned to 1 thread; host reports {os.cpu_count()} cpus",
+        "cpu_model": cpu_model(),
+        "host_cpus": os.cpu_count(),
+        "linearity": {"half_context_tokens_per_s": rate_half, "full_context_tokens_per_s": rate,
+                      "ratio_full_over_half": rate / rate_half},
+        "sample": f"layer 0: {streams} whole (sequence, KV head) streams x {Q} query heads, {tokens} tokens, "
+                  f"{dt:.1f} s of oracle time (page downloads excluded), after {s_half} streams cut to half their "
+                  f"pages ({t_half} tokens, {dt_half:.1f} s) for the linearity check; numpy oracle of reference "
+                  f"cpu_ref, one thread (BLAS pinned to 1), on {cpu_model()} ({os.cpu_count()} cpus visible)",
     }
 
 
@@ -245,13 +268,29 @@ def main():
         torch.cuda.synchronize()
         return a.elapsed_time(b)
 
-    # (1) the benchmark proper: exactly K whole steps
-    ms_step = timed(wl.step, args.steps) / args.steps
+    def per_call(fn, n):
+        """ms of each of n calls, from events recorded between the calls
+        (each call is a whole graph replay: never between kernels)."""
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        for i in range(n):
+            fn()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        return np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(n)])
 
-    # (2) the dominant kernel alone: the K steps' decode launches back to
+    # (1) the benchmark proper: exactly K whole steps between two syncs
+    ms_step = timed(wl.step, args.steps) / args.steps
+    # (1b) the per-step distribution: >= 50 steps, an event between steps
+    n_med = max(50, args.steps)
+    step_ms = per_call(wl.step, n_med)
+
+    # (2) the dominant kernel alone: the decode launches of a step back to
     # back (partials left in the workspace), then (3) the merges alone; each
     # as a graph of one step's launches (unless --eager), so that a short
-    # kernel is not timed at the host's launch rate
+    # kernel is not timed at the host's launch rate; medians over >= 50
+    # replays, an event between replays
     def decode_all():
         for l in range(L):
             wl.decode_kernel(l)
@@ -263,16 +302,22 @@ def main():
     if not args.eager:
         g_dec, g_merge = wl.capture_fn(decode_all), wl.capture_fn(merge_all)
         decode_all, merge_all = g_dec.replay, g_merge.replay
-    launch_ms = timed(decode_all, args.steps) / (args.steps * L)
-    merge_ms = timed(merge_all, args.steps) / (args.steps * L)
+    dec_ms = per_call(decode_all, n_med) / L
+    merge_ms_all = per_call(merge_all, n_med) / L
+    # roofline.achieved uses the mean launch time (what a kernel trace's
+    # average gives); the median is reported beside it
+    launch_ms = float(np.mean(dec_ms))
+    merge_ms = float(np.mean(merge_ms_all))
 
     bytes_step = wl.algorithmic_bytes_per_step()
     pos_step = wl.token_positions_per_step()
     value = pos_step / (ms_step / 1e3)
+    ms_step_median = float(np.median(step_ms))
     gbps = bytes_step / (ms_step / 1e3) / 1e9
     bytes_launch = bytes_step / L
     achieved = bytes_launch / (launch_ms / 1e3) / 1e9
-    log(f"{ms_step:.3f} ms/step, {value / 1e9:.3f} G tokens/s, {gbps:.0f} GB/s over the step; "
+    log(f"{ms_step:.3f} ms/step (median {ms_step_median:.3f} over {n_med}), {value / 1e9:.3f} G tokens/s, "
+        f"{gbps:.0f} GB/s over the step; "
         f"decode kernel {launch_ms * 1e3:.1f} us -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBPS:.1%} of peak), "
         f"merge {merge_ms * 1e3:.1f} us")
 
@@ -291,6 +336,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms_step,
+        "ms_per_step_median": ms_step_median,
+        "ms_per_step_p10_p90": [float(np.percentile(step_ms, 10)), float(np.percentile(step_ms, 90))],
+        "median_steps": n_med,
+        "value_at_median_step": pos_step / (ms_step_median / 1e3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -326,6 +375,10 @@ def main():
             "kernel": ("decode_mfma_kernel" if args.decode_path == "auto" else "decode_generic_kernel")
                       + " (dc_decode_paged, one launch per layer)",
             "launch_us": launch_ms * 1e3,
+            "launch_us_stat": f"mean over {n_med} replays of one step's {L} decode launches (event per replay)",
+            "launch_us_median": float(np.median(dec_ms)) * 1e3,
+            "launch_us_p10_p90": [float(np.percentile(dec_ms, 10)) * 1e3, float(np.percentile(dec_ms, 90)) * 1e3],
+            "frac_at_median_launch": bytes_launch / (float(np.median(dec_ms)) / 1e3) / 1e9 / HBM_PEAK_GBPS,
             "bytes_per_launch": bytes_launch,
             "merge_us": merge_ms * 1e3,
             "decode_path": args.decode_path,

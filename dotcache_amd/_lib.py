@@ -62,6 +62,10 @@ SIGNATURES = {
     "dc_encode_rows": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, Pool, C.c_void_p]),
     "dc_score_pages": (C.c_int, [Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_int64, C.c_void_p]),
     "dc_mix_pages": (C.c_int, [Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int64, C.c_void_p, C.c_int32, C.c_void_p]),
+    "dc_score_pages_grouped": (C.c_int, [Pool, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
+                                         C.c_int32, C.c_void_p, C.c_int64, C.c_void_p]),
+    "dc_mix_pages_grouped": (C.c_int, [Pool, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
+                                       C.c_int32, C.c_int64, C.c_void_p, C.c_int32, C.c_void_p]),
     "dc_softmax_rows": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int64, C.c_void_p]),
     "dc_page_summaries": (C.c_int, [Pool, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p]),

@@ -395,15 +395,57 @@ def _grouped_inputs(query_groups, key_pages_by_group, value_pages_by_group):
 def decode_grouped_multiquery_step_prepared_hip_tensor(query_groups, key_pages_by_group, value_pages_by_group, *,
                                                        trace: ExecutionTrace | None = None, **_ignored):
     """Per KV group: (logits [G, Q, T], weights [G, Q, T], output [G, Q, head_dim])
-    -- reference ``decode_grouped_multiquery_step_prepared_cuda_tensor``.
-    Groups must hold the same token counts, as in the reference."""
+    -- reference ``decode_grouped_multiquery_step_prepared_cuda_tensor``
+    (``torch_cuda.py:131-143`` over ``torch_mps.py:4110-4273``).  One batched
+    pass for all groups: one grouped score launch, one softmax over the
+    G x Q rows, one grouped mix launch.  Groups must hold the same token
+    counts, as in the reference."""
     torch = _torch()
     _grouped_inputs(query_groups, key_pages_by_group, value_pages_by_group)
-    res = [decode_multi_query_step_hip_tensor(q, k, v, trace=trace)
-           for q, k, v in zip(query_groups, key_pages_by_group, value_pages_by_group)]
-    if len({r[0].shape for r in res}) != 1:
+    G = len(key_pages_by_group)
+    counts = [len(g) for g in key_pages_by_group]
+    if counts != [len(g) for g in value_pages_by_group]:
+        raise ValueError("key_pages_by_group and value_pages_by_group must align")
+    flat_k = [p for grp in key_pages_by_group for p in grp]
+    flat_v = [p for grp in value_pages_by_group for p in grp]
+    kpool, kids, kprep = _one_pool(flat_k, trace)
+    vpool, vids, vprep = _one_pool(flat_v, trace)
+    _record_reads(trace, kprep + vprep, "decode_grouped_multiquery_step")
+    ktok, vtok = kpool.tokens_of(kids), vpool.tokens_of(vids)
+    if not np.array_equal(ktok, vtok):
+        raise ValueError("key and value pages must hold the same token counts")
+    bounds = np.zeros(G + 1, dtype=np.int64)
+    bounds[1:] = np.cumsum(counts)
+    totals = [int(ktok[bounds[g]:bounds[g + 1]].sum()) for g in range(G)]
+    dev = kpool.device
+    q = torch.stack([_queries_tensor(x, kpool.geometry.head_dim, dev) for x in query_groups]).contiguous()  # [G, Q, hd]
+    Q, hd = int(q.shape[1]), int(q.shape[2])
+    if len(set(totals)) != 1:
         raise ValueError("all query groups must have the same query count and token count for batched grouped decode")
-    return torch.stack([r[0] for r in res]), torch.stack([r[1] for r in res]), torch.stack([r[2] for r in res])
+    T = totals[0]
+    # token offsets within each group, the group of every page
+    offsets = np.zeros(len(kids) + 1, dtype=np.int32)
+    for g in range(G):
+        seg = ktok[bounds[g]:bounds[g + 1]]
+        offsets[bounds[g] + 1:bounds[g + 1] + 1] = np.cumsum(seg)
+    page_group = np.repeat(np.arange(G, dtype=np.int32), counts)
+    kids_d, vids_d = torch.from_numpy(kids).to(dev), torch.from_numpy(vids).to(dev)
+    off_d = torch.from_numpy(offsets[:-1].copy()).to(dev)
+    grp_d = torch.from_numpy(page_group).to(dev)
+    gp_d = torch.from_numpy(bounds.astype(np.int32)).to(dev)
+    logits = torch.empty((G, Q, T), dtype=torch.float32, device=dev)
+    stream = C.c_void_p(current_stream_ptr())
+    L = _lib.lib()
+    _lib.check(L.dc_score_pages_grouped(kpool.c_pool(), C.c_void_p(kids_d.data_ptr()), C.c_void_p(off_d.data_ptr()),
+                                        C.c_void_p(grp_d.data_ptr()), G, len(kids), C.c_void_p(q.data_ptr()), Q,
+                                        C.c_void_p(logits.data_ptr()), T, stream), "dc_score_pages_grouped")
+    weights = logits.clone()
+    _lib.check(L.dc_softmax_rows(C.c_void_p(weights.data_ptr()), G * Q, T, T, stream), "dc_softmax_rows")
+    out = torch.empty((G, Q, hd), dtype=torch.float32, device=dev)
+    _lib.check(L.dc_mix_pages_grouped(vpool.c_pool(), C.c_void_p(vids_d.data_ptr()), C.c_void_p(off_d.data_ptr()),
+                                      C.c_void_p(gp_d.data_ptr()), G, len(vids), C.c_void_p(weights.data_ptr()), Q, T,
+                                      C.c_void_p(out.data_ptr()), 0, stream), "dc_mix_pages_grouped")
+    return logits, weights, out
 
 
 decode_grouped_multiquery_step_hip_tensor = decode_grouped_multiquery_step_prepared_hip_tensor

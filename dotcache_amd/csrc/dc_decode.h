@@ -20,6 +20,7 @@ struct DecodeArgs {
   const void* queries;
   int32_t queries_dtype;
   float q_scale;
+  int32_t n_seqs;
   int32_t n_kv_heads;
   int32_t n_q;
   float* out;
@@ -27,6 +28,13 @@ struct DecodeArgs {
   float* part_ml;   // [max_partials][n_q][2]  (m, l) in the log2 domain
   int64_t max_partials;
 };
+
+// A work item naming a sequence, KV head or page range outside the call's
+// shapes is skipped, not read: a fault guard only (hosts validate plans).
+__device__ __forceinline__ bool item_in_bounds(const dc_work_item& it, const DecodeArgs& a) {
+  return it.seq >= 0 && it.seq < a.n_seqs && it.kv_head >= 0 && it.kv_head < a.n_kv_heads && it.page_begin >= 0 &&
+         it.page_begin <= it.page_end && it.page_end <= a.table_stride;
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -56,6 +56,7 @@ __device__ __forceinline__ float score_partial_m0(const uint8_t* blob, const dc_
 
 __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) {
   const dc_work_item it = a.items[blockIdx.x];
+  if (!item_in_bounds(it, a)) return;
   const dc_page_geometry geo = a.kpool.geometry, vgeo = a.vpool.geometry;
   const int32_t hd = geo.head_dim, gs = geo.group_size;
   const int32_t G = (hd + gs - 1) / gs, phd = G * gs;
@@ -202,7 +203,7 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
 // (log2 domain).
 template <int V>
 __global__ void __launch_bounds__(256) merge_kernel(const dc_merge_item* __restrict__ merges, const float* part_o,
-                                                    const float* part_ml, float* out, int32_t n_kv_heads,
+                                                    const float* part_ml, float* out, int32_t n_seqs, int32_t n_kv_heads,
                                                     int32_t nq, int32_t hd, int64_t max_partials) {
   struct Vec {
     float v[V];
@@ -212,6 +213,7 @@ __global__ void __launch_bounds__(256) merge_kernel(const dc_merge_item* __restr
   const dc_merge_item mi = merges[blockIdx.x];
   const int j = blockIdx.y, t = threadIdx.x;
   if (mi.partial_begin < 0 || mi.count <= 0 || int64_t(mi.partial_begin) + mi.count > max_partials) return;
+  if (mi.seq < 0 || mi.seq >= n_seqs || mi.kv_head < 0 || mi.kv_head >= n_kv_heads) return;
   const int C = hd / V, R = 256 / C;  // hd <= 256, so R >= 1
   const int row = t / C, col = t - row * C;
   const float* ml = part_ml + (int64_t(mi.partial_begin) * nq + j) * 2;             // partial s at ml[2 nq s]
@@ -311,10 +313,10 @@ int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_mer
   const bool vec4 = (hd & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.part_o) | reinterpret_cast<uintptr_t>(a.out)) & 15) == 0;
   const dim3 grid(uint32_t(n_merges), uint32_t(a.n_q));
   if (vec4)
-    hipLaunchKernelGGL(merge_kernel<4>, grid, dim3(256), 0, stream, merges, a.part_o, a.part_ml, a.out, a.n_kv_heads,
+    hipLaunchKernelGGL(merge_kernel<4>, grid, dim3(256), 0, stream, merges, a.part_o, a.part_ml, a.out, a.n_seqs, a.n_kv_heads,
                        a.n_q, hd, a.max_partials);
   else
-    hipLaunchKernelGGL(merge_kernel<1>, grid, dim3(256), 0, stream, merges, a.part_o, a.part_ml, a.out, a.n_kv_heads,
+    hipLaunchKernelGGL(merge_kernel<1>, grid, dim3(256), 0, stream, merges, a.part_o, a.part_ml, a.out, a.n_seqs, a.n_kv_heads,
                        a.n_q, hd, a.max_partials);
   return check_hip(hipGetLastError(), "merge_kernel launch");
 }
@@ -359,6 +361,7 @@ extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_
   a.queries = queries;
   a.queries_dtype = queries_dtype;
   a.q_scale = query_scale;
+  a.n_seqs = n_seqs;
   a.n_kv_heads = n_kv_heads;
   a.n_q = n_q;
   a.out = out;
@@ -389,6 +392,7 @@ extern "C" int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const
   const int64_t n_partials = workspace_bytes / per_partial;
   if (!workspace || n_partials <= 0) return dc::fail(DC_ESPACE, "dc_lse_merge: no partials in the workspace");
   dc::DecodeArgs a{};
+  a.n_seqs = n_seqs;
   a.n_kv_heads = n_kv_heads;
   a.n_q = n_q;
   a.out = out;

@@ -174,6 +174,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   using KB1 = std::integral_constant<int, 1>;
 
   const dc_work_item it = a.items[blockIdx.x];
+  if (!item_in_bounds(it, a)) return;
   const int lane = threadIdx.x;
   const int r = lane & 15, kb = lane >> 4;
   const int nq = a.n_q;

@@ -12,13 +12,21 @@ namespace dc {
 
 constexpr int kScoreQ = 8;  // queries scored per pass
 
-// grid.x = page index, grid.y = query chunk; one thread per token.
+// grid.x = page index, grid.y = query chunk; one thread per token.  With
+// page_group, page i is scored against the queries of group page_group[i]
+// (queries [n_groups][n_queries][hd]) into logits rows
+// group * n_queries + q; without it every page belongs to group 0.
 __global__ void __launch_bounds__(256) score_pages_kernel(dc_pool pool, const int32_t* __restrict__ page_ids,
                                                           const int32_t* __restrict__ token_offsets,
-                                                          const float* __restrict__ queries, int32_t n_queries,
-                                                          float* __restrict__ logits, int64_t logits_stride) {
+                                                          const int32_t* __restrict__ page_group, int32_t n_groups,
+                                                          const float* __restrict__ queries_all, int32_t n_queries,
+                                                          float* __restrict__ logits_all, int64_t logits_stride) {
   const int32_t i = blockIdx.x;
   const int32_t q0 = blockIdx.y * kScoreQ;
+  const int32_t grp = page_group ? page_group[i] : 0;
+  if (grp < 0 || grp >= n_groups) return;
+  const float* queries = queries_all + int64_t(grp) * n_queries * pool.geometry.head_dim;
+  float* logits = logits_all + int64_t(grp) * n_queries * logits_stride;
   const int32_t pid = page_ids[i];
   if (pid < 0 || pid >= pool.n_descs) return;
   const dc_page_desc d = pool.descs[pid];
@@ -77,10 +85,13 @@ __global__ void __launch_bounds__(256) score_pages_kernel(dc_pool pool, const in
   }
 }
 
-// grid.x = query, grid.y = channel block; one thread per channel, looping
-// over every page and token.
+// grid.x = query row (group * n_queries + q), grid.y = channel block; one
+// thread per channel, looping over the pages of the row's group
+// [group_pages[g], group_pages[g + 1]) (every page without group_pages) and
+// their tokens.
 __global__ void __launch_bounds__(256) mix_pages_kernel(dc_pool pool, const int32_t* __restrict__ page_ids,
                                                         const int32_t* __restrict__ token_offsets, int32_t n_pages,
+                                                        const int32_t* __restrict__ group_pages, int32_t n_queries,
                                                         const float* __restrict__ weights, int64_t weights_stride,
                                                         float* __restrict__ out, int32_t accumulate) {
   const int32_t q = blockIdx.x;
@@ -88,8 +99,14 @@ __global__ void __launch_bounds__(256) mix_pages_kernel(dc_pool pool, const int3
   const dc_page_geometry geo = pool.geometry;
   if (c >= geo.head_dim) return;
   const float* w = weights + int64_t(q) * weights_stride;
+  int32_t i0 = 0, i1 = n_pages;
+  if (group_pages) {
+    const int32_t g = q / n_queries;
+    i0 = group_pages[g] < 0 ? 0 : group_pages[g];
+    i1 = group_pages[g + 1] > n_pages ? n_pages : group_pages[g + 1];
+  }
   float acc = 0.f;
-  for (int32_t i = 0; i < n_pages; ++i) {
+  for (int32_t i = i0; i < i1; ++i) {
     const int32_t pid = page_ids[i];
     if (pid < 0 || pid >= pool.n_descs) continue;
     const dc_page_desc d = pool.descs[pid];
@@ -106,32 +123,65 @@ __global__ void __launch_bounds__(256) mix_pages_kernel(dc_pool pool, const int3
 
 }  // namespace dc
 
+static int score_launch(const dc_pool& pool, const int32_t* page_ids, const int32_t* token_offsets,
+                        const int32_t* page_group, int32_t n_groups, int32_t n_pages, const float* queries,
+                        int32_t n_queries, float* logits, int64_t logits_stride, hipStream_t stream, const char* who) {
+  if (int rc = dc::validate_geometry(pool.geometry)) return rc;
+  if (n_pages < 0 || n_queries < 0 || n_groups <= 0) return dc::fail(DC_EINVAL, "%s: bad counts", who);
+  if (n_pages == 0 || n_queries == 0) return DC_OK;
+  if (!page_ids || !token_offsets || !queries || !logits || !pool.arena || !pool.descs)
+    return dc::fail(DC_EINVAL, "%s: null pointer", who);
+  const uint32_t qchunks = uint32_t((n_queries + dc::kScoreQ - 1) / dc::kScoreQ);
+  hipLaunchKernelGGL(dc::score_pages_kernel, dim3(uint32_t(n_pages), qchunks), dim3(128), 0, stream, pool, page_ids,
+                     token_offsets, page_group, n_groups, queries, n_queries, logits, logits_stride);
+  return dc::check_hip(hipGetLastError(), who);
+}
+
+static int mix_launch(const dc_pool& pool, const int32_t* page_ids, const int32_t* token_offsets, int32_t n_pages,
+                      const int32_t* group_pages, int32_t n_groups, const float* weights, int32_t n_queries,
+                      int64_t weights_stride, float* out, int32_t accumulate, hipStream_t stream, const char* who) {
+  if (int rc = dc::validate_geometry(pool.geometry)) return rc;
+  if (n_pages < 0 || n_queries < 0 || n_groups <= 0) return dc::fail(DC_EINVAL, "%s: bad counts", who);
+  if (n_queries == 0) return DC_OK;
+  if (!weights || !out || (n_pages > 0 && (!page_ids || !token_offsets || !pool.arena || !pool.descs)))
+    return dc::fail(DC_EINVAL, "%s: null pointer", who);
+  const uint32_t cblocks = uint32_t((pool.geometry.head_dim + 255) / 256);
+  hipLaunchKernelGGL(dc::mix_pages_kernel, dim3(uint32_t(n_groups) * uint32_t(n_queries), cblocks), dim3(256), 0,
+                     stream, pool, page_ids, token_offsets, n_pages, group_pages, n_queries, weights, weights_stride,
+                     out, accumulate);
+  return dc::check_hip(hipGetLastError(), who);
+}
+
 extern "C" int dc_score_pages(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets, int32_t n_pages,
                               const float* queries, int32_t n_queries, float* logits, int64_t logits_stride,
                               dc_stream_t stream) {
-  if (int rc = dc::validate_geometry(pool.geometry)) return rc;
-  if (n_pages < 0 || n_queries < 0) return dc::fail(DC_EINVAL, "counts must be non-negative");
-  if (n_pages == 0 || n_queries == 0) return DC_OK;
-  if (!page_ids || !token_offsets || !queries || !logits || !pool.arena || !pool.descs)
-    return dc::fail(DC_EINVAL, "dc_score_pages: null pointer");
-  const uint32_t qchunks = uint32_t((n_queries + dc::kScoreQ - 1) / dc::kScoreQ);
-  hipLaunchKernelGGL(dc::score_pages_kernel, dim3(uint32_t(n_pages), qchunks), dim3(128), 0, hipStream_t(stream),
-                     pool, page_ids, token_offsets, queries, n_queries, logits, logits_stride);
-  return dc::check_hip(hipGetLastError(), "dc_score_pages launch");
+  return score_launch(pool, page_ids, token_offsets, nullptr, 1, n_pages, queries, n_queries, logits, logits_stride,
+                      hipStream_t(stream), "dc_score_pages");
 }
 
 extern "C" int dc_mix_pages(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets, int32_t n_pages,
                             const float* weights, int32_t n_queries, int64_t weights_stride, float* out,
                             int32_t accumulate, dc_stream_t stream) {
-  if (int rc = dc::validate_geometry(pool.geometry)) return rc;
-  if (n_pages < 0 || n_queries < 0) return dc::fail(DC_EINVAL, "counts must be non-negative");
-  if (n_queries == 0) return DC_OK;
-  if (!weights || !out || (n_pages > 0 && (!page_ids || !token_offsets || !pool.arena || !pool.descs)))
-    return dc::fail(DC_EINVAL, "dc_mix_pages: null pointer");
-  const uint32_t cblocks = uint32_t((pool.geometry.head_dim + 255) / 256);
-  hipLaunchKernelGGL(dc::mix_pages_kernel, dim3(uint32_t(n_queries), cblocks), dim3(256), 0, hipStream_t(stream),
-                     pool, page_ids, token_offsets, n_pages, weights, weights_stride, out, accumulate);
-  return dc::check_hip(hipGetLastError(), "dc_mix_pages launch");
+  return mix_launch(pool, page_ids, token_offsets, n_pages, nullptr, 1, weights, n_queries, weights_stride, out,
+                    accumulate, hipStream_t(stream), "dc_mix_pages");
+}
+
+extern "C" int dc_score_pages_grouped(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets,
+                                      const int32_t* page_group, int32_t n_groups, int32_t n_pages,
+                                      const float* queries, int32_t n_queries, float* logits, int64_t logits_stride,
+                                      dc_stream_t stream) {
+  if (n_pages > 0 && !page_group) return dc::fail(DC_EINVAL, "dc_score_pages_grouped: null page_group");
+  return score_launch(pool, page_ids, token_offsets, page_group, n_groups, n_pages, queries, n_queries, logits,
+                      logits_stride, hipStream_t(stream), "dc_score_pages_grouped");
+}
+
+extern "C" int dc_mix_pages_grouped(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets,
+                                    const int32_t* group_pages, int32_t n_groups, int32_t n_pages,
+                                    const float* weights, int32_t n_queries, int64_t weights_stride, float* out,
+                                    int32_t accumulate, dc_stream_t stream) {
+  if (!group_pages) return dc::fail(DC_EINVAL, "dc_mix_pages_grouped: null group_pages");
+  return mix_launch(pool, page_ids, token_offsets, n_pages, group_pages, n_groups, weights, n_queries, weights_stride,
+                    out, accumulate, hipStream_t(stream), "dc_mix_pages_grouped");
 }
 
 namespace dc {

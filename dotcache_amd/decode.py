@@ -43,7 +43,44 @@ class DecodePlan:
     n_merges: int
     n_partials: int
     pages_per_split: int
-    host_items: np.ndarray
+    host_items: np.ndarray            # int32 [n_items, 8]: dc_work_item fields
+    host_merges: np.ndarray | None = None  # int32 [n_merges, 4]: dc_merge_item fields
+    checked: set = None               # (seq_pages, n_kv_heads, table_stride) keys already validated
+
+    def check(self, seq_pages: np.ndarray, n_kv_heads: int, table_stride: int) -> None:
+        """Raise ValueError unless every work item and merge item of the plan
+        stays inside these shapes: sequence < n_seqs, KV head < n_kv_heads,
+        pages within the sequence's count (and so within the page table),
+        partial slots below n_partials, and device buffers as long as the
+        counts.  The kernels read items without checking them against the
+        tables, so a plan built for other shapes must not reach them.
+        Validated once per shape key."""
+        sp = np.asarray(seq_pages, dtype=np.int64)
+        key = (sp.tobytes(), int(n_kv_heads), int(table_stride))
+        if self.checked is None:
+            self.checked = set()
+        if key in self.checked:
+            return
+        B = sp.size
+        it = np.asarray(self.host_items, dtype=np.int64).reshape(-1, 8)
+        if it.shape[0] != self.n_items or self.items.numel() < 32 * self.n_items:
+            raise ValueError("plan: work item count does not match its device buffer")
+        seq, head, pb, pe, part = it[:, 0], it[:, 1], it[:, 2], it[:, 3], it[:, 4]
+        if np.any((seq < 0) | (seq >= B)) or np.any((head < 0) | (head >= n_kv_heads)):
+            raise ValueError(f"plan: a work item names a sequence or KV head outside [{B}] x [{n_kv_heads}]")
+        limit = np.minimum(sp[np.clip(seq, 0, max(B - 1, 0))], int(table_stride))
+        if np.any(pb < 0) or np.any(pe < pb) or np.any(pe > limit):
+            raise ValueError("plan: a work item's pages lie outside its sequence's page table")
+        if np.any(part >= self.n_partials):
+            raise ValueError("plan: a work item names a partial slot past n_partials")
+        if self.n_merges:
+            m = np.asarray(self.host_merges, dtype=np.int64).reshape(-1, 4)
+            if m.shape[0] != self.n_merges or self.merges is None or self.merges.numel() < 16 * self.n_merges:
+                raise ValueError("plan: merge item count does not match its device buffer")
+            if (np.any((m[:, 0] < 0) | (m[:, 0] >= B)) or np.any((m[:, 1] < 0) | (m[:, 1] >= n_kv_heads))
+                    or np.any(m[:, 2] < 0) or np.any(m[:, 3] <= 0) or np.any(m[:, 2] + m[:, 3] > self.n_partials)):
+                raise ValueError("plan: a merge item lies outside the shapes or the partial slots")
+        self.checked.add(key)
 
 
 _plan_cache: dict = {}
@@ -108,9 +145,10 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
                           C.addressof(merges), nm.value, C.byref(nm), C.byref(npart))
     _lib.check(st, "dc_plan_decode")
     host_items = np.frombuffer(bytes(items), dtype=np.int32).reshape(-1, 8)[: ni.value].copy()
+    host_merges = np.frombuffer(bytes(merges), dtype=np.int32).reshape(-1, 4)[: nm.value].copy()
     dev_items = torch.frombuffer(bytearray(bytes(items)), dtype=torch.uint8).to(device)
     dev_merges = torch.frombuffer(bytearray(bytes(merges)), dtype=torch.uint8).to(device) if nm.value else None
-    plan = DecodePlan(dev_items, dev_merges, ni.value, nm.value, npart.value, pps, host_items)
+    plan = DecodePlan(dev_items, dev_merges, ni.value, nm.value, npart.value, pps, host_items, host_merges)
     if len(_plan_cache) > 256:
         _plan_cache.clear()
     _plan_cache[key] = plan
@@ -191,6 +229,7 @@ def decode_paged(
                 raise ValueError("key and value pages must hold the same token counts")
     if plan is None:
         plan = make_plan(sp, H, pages_per_split, device=queries.device)
+    plan.check(sp, H, stride)
     if not queries.is_contiguous():
         queries = queries.contiguous()
     if out is None:
@@ -216,6 +255,9 @@ def merge_partials(plan: DecodePlan, out, workspace) -> None:
     if plan.n_merges == 0:
         return
     B, H, Q, hd = (int(x) for x in out.shape)
+    m = np.asarray(plan.host_merges, dtype=np.int64).reshape(-1, 4)
+    if np.any((m[:, 0] < 0) | (m[:, 0] >= B)) or np.any((m[:, 1] < 0) | (m[:, 1] >= H)):
+        raise ValueError("plan: a merge item names a sequence or KV head outside the output")
     st = _lib.lib().dc_lse_merge(C.c_void_p(plan.merges.data_ptr()), plan.n_merges, C.c_void_p(workspace.data_ptr()),
                                  int(workspace.numel()), B, H, Q, hd, C.c_void_p(out.data_ptr()),
                                  C.c_void_p(current_stream_ptr()))

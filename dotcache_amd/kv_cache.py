@@ -18,17 +18,25 @@ device-to-host copy.  Here every (layer, sequence, KV head) stream owns:
   the reference's ``encode_page`` of the same fp32 rows
   (``model_kv_cache.py:788-830``).
 
-Page modes follow ``DotCacheConfig.resolve_page_mode`` (per-layer and
-per-head overrides, reference ``config.py:390-414``).  Several sequences
+Page modes are chosen as the reference's numpy cache chooses them.  A kind
+without mode or policy overrides takes ``DotCacheConfig.resolve_page_mode``.
+A kind with any override takes ``choose_page_mode`` under the stream's layer
+policy (reference ``model_kv_cache.py:3164-3185`` for prefill pages,
+``:789-810`` for pages finalised by ``append_step``), with the token age
+``sequence_length - token_start - 1`` of the page: young pages of a tier
+policy become M3 (the recent window), and the header fields
+``policy_id`` / ``sensitivity_tier`` / ``fallback_reason`` / ``age_bucket``
+record the choice.  Page statistics (``observe_page``) are computed on the
+device, only when a candidate needs them.  Several sequences
 (``batch_size``) share the pools and decode in one launch per layer.
 """
 from __future__ import annotations
 
 import numpy as np
 
-from .config import DotCacheConfig
+from .config import DotCacheConfig, observe_page
 from .decode import decode_paged, make_plan, workspace_bytes
-from .encode import resolve_encode_spec
+from .encode import make_header, resolve_encode_spec
 from .page_pool import DevicePagePool, PoolGeometry, page_format_of
 
 
@@ -94,6 +102,7 @@ class DevicePagedKVCache:
         self._seq_len = np.zeros((L, B), dtype=np.int64)    # tokens cached per (layer, sequence)
         self._tail_start = np.zeros((L, B), dtype=np.int64)  # absolute index of each tail's first token
         self._tables = [None] * L  # (k_table, v_table, seq_pages) on the device, rebuilt when pages change
+        self._spec_memo: dict = {}
         self._workspace = None
 
     # ---- formats -----------------------------------------------------------
@@ -101,6 +110,27 @@ class DevicePagedKVCache:
         spec = self._specs[kind]
         mode = self.config.resolve_page_mode(kind=kind, layer_id=layer_id, kv_head_id=kv_head_id)
         return page_format_of(mode, spec["scheme"], spec["bits"], spec["escape_dtype"])
+
+    def _page_spec(self, kind: str, layer_id: int, kv_head_id: int, token_start: int, sequence_length: int,
+                   rows) -> dict:
+        """Encode spec (mode, bits, scheme, escape dtype, policy header
+        fields) of one full page whose fp32 device rows are ``rows [P, hd]``:
+        ``choose_page_mode`` when the kind has overrides, else the layer's
+        resolved mode (reference ``model_kv_cache.py:3164-3185``)."""
+        cfg = self.config
+        if not cfg.chooses_page_modes(kind):  # the mode depends on (kind, layer, head) only
+            key = (kind, int(layer_id), int(kv_head_id))
+            hit = self._spec_memo.get(key)
+            if hit is None:
+                mode = cfg.resolve_page_mode(kind=kind, layer_id=layer_id, kv_head_id=kv_head_id)
+                hit = self._spec_memo[key] = resolve_encode_spec(cfg, kind=kind, mode=mode)
+            return hit
+        chosen = cfg.select_page_mode(kind=kind, layer_id=layer_id, kv_head_id=kv_head_id, token_start=token_start,
+                                      sequence_length=sequence_length, stats=lambda: observe_page(rows))
+        if chosen.mode not in ("M0", "M3"):
+            raise ValueError(f"the {kind} page policy of layer {layer_id} chose mode {chosen.mode} "
+                             f"(token_start {token_start}), which hip_mi355x does not encode")
+        return resolve_encode_spec(cfg, kind=kind, page_mode=chosen)
 
     def _pool(self, kind: str) -> DevicePagePool:
         return self.k_pool if kind == "K" else self.v_pool
@@ -131,18 +161,27 @@ class DevicePagedKVCache:
         if len(page_ids):
             self._pool(kind).encode_rows(rows, page_ids.astype(np.int32), slots.astype(np.int32))
 
-    def _finalise_pages(self, kind: str, layer_id: int, rows, token_stream: np.ndarray) -> None:
+    def _finalise_pages(self, kind: str, layer_id: int, rows, token_stream: np.ndarray, token_starts: np.ndarray,
+                        sequence_lengths: np.ndarray) -> None:
         """Encode full pages: ``rows [n_pages * P, hd]`` fp32, page i of
-        stream ``token_stream[i]`` (index b * H + h)."""
+        stream ``token_stream[i]`` (index b * H + h) starting at absolute
+        token ``token_starts[i]`` of a context of ``sequence_lengths[i]``
+        tokens (the page-mode choice reads both)."""
         P, H = self.config.tokens_per_page, self.num_key_value_heads
         pool = self._pool(kind)
-        ids = np.empty(len(token_stream), dtype=np.int64)
-        for fmt_bits in {self._page_format(kind, layer_id, int(s) % H) for s in token_stream}:
-            sel = [i for i, s in enumerate(token_stream) if self._page_format(kind, layer_id, int(s) % H) == fmt_bits]
+        n = len(token_stream)
+        specs = [self._page_spec(kind, layer_id, int(s) % H, int(t0), int(sl), rows[i * P:(i + 1) * P])
+                 for i, (s, t0, sl) in enumerate(zip(token_stream, token_starts, sequence_lengths))]
+        fmts = [page_format_of(sp["mode"], sp["scheme"], sp["bits"], sp["escape_dtype"]) for sp in specs]
+        ids = np.empty(n, dtype=np.int64)
+        for fmt_bits in set(fmts):
+            sel = [i for i in range(n) if fmts[i] == fmt_bits]
             ids[sel] = pool.allocate(*fmt_bits, len(sel), tokens=P)
-        self._encode(kind, rows, np.repeat(ids, P), np.tile(np.arange(P), len(ids)))
-        for pid, s in zip(ids.tolist(), token_stream.tolist()):
+        self._encode(kind, rows, np.repeat(ids, P), np.tile(np.arange(P), n))
+        for i, (pid, s) in enumerate(zip(ids.tolist(), token_stream.tolist())):
             self._pages[kind][layer_id][s // H][s % H].append(pid)
+            pool.headers[pid] = make_header(self.config, specs[i], kind=kind, layer_id=layer_id, kv_head_id=s % H,
+                                            token_start=int(token_starts[i]), token_count=P)
 
     def _write_tail(self, kind: str, layer_id: int, rows, first_slot: int) -> None:
         """Rows ``[B, H, n, hd]`` into tail slots ``first_slot ..`` of every
@@ -179,10 +218,13 @@ class DevicePagedKVCache:
         B, H, P, hd = self.batch_size, self.num_key_value_heads, self.config.tokens_per_page, self.config.head_dim
         full = (T // P) * P
         if full:
-            # page-major rows: stream (b, h), page i, slot j
+            # page-major rows: stream (b, h), page i, slot j; page i starts at
+            # absolute token ctx - T + i P of a ctx-token context
             streams = np.repeat(np.arange(B * H), full // P)
+            starts = np.tile((ctx - T) + P * np.arange(full // P), B * H)
             for kind, x in (("K", keys), ("V", values)):
-                self._finalise_pages(kind, lid, x[:, :, :full].reshape(B * H * full, hd), streams)
+                self._finalise_pages(kind, lid, x[:, :, :full].reshape(B * H * full, hd), streams, starts,
+                                     np.full(len(streams), ctx))
         for kind, x in (("K", keys), ("V", values)):
             self._write_tail(kind, lid, x[:, :, full:], 0)
         self._seq_len[lid, :] = ctx
@@ -210,10 +252,13 @@ class DevicePagedKVCache:
             done += take
             self._seq_len[lid, :] += take
             if fill + take == P:  # every stream's tail is full: encode it into a page
+                # the page's context is the whole step's (reference
+                # model_kv_cache.py:3887-3892 passes token_index + n)
                 streams = np.arange(B * H)
+                starts = np.repeat(self._tail_start[lid], H)
                 for kind in ("K", "V"):
                     rows = self._tail_rows[kind][lid].reshape(B * H * P, hd)
-                    self._finalise_pages(kind, lid, rows, streams)
+                    self._finalise_pages(kind, lid, rows, streams, starts, np.full(B * H, int(token_index) + n))
                     self._pool(kind).set_tokens(self._tail_page[kind][lid].reshape(-1), 0)
                 self._tail_start[lid, :] = self._seq_len[lid, :]
             self._tables[lid] = None
@@ -307,6 +352,13 @@ class DevicePagedKVCache:
     def page_ids(self, layer_id: int, sequence: int, kv_head_id: int, kind: str = "K") -> list[int]:
         """Finalised page ids of one stream, oldest first (the tail excluded)."""
         return list(self._pages[kind][self._check_layer(layer_id)][int(sequence)][int(kv_head_id)])
+
+    def page(self, layer_id: int, sequence: int, kv_head_id: int, index: int, kind: str = "K"):
+        """Finalised page ``index`` of one stream as a host ``EncodedPage``
+        with the header the reference's cache gives it (token_start, mode
+        and the policy fields)."""
+        pid = self.page_ids(layer_id, sequence, kv_head_id, kind)[index]
+        return self._pool(kind).download_page(pid, kind=kind)
 
     def tail_page_id(self, layer_id: int, sequence: int, kv_head_id: int, kind: str = "K") -> int:
         return int(self._tail_page[kind][self._check_layer(layer_id), int(sequence), int(kv_head_id)])

@@ -135,7 +135,15 @@ def relevance_scores(query, sketch, minima, maxima, mode: str):
     torch = _torch()
     if mode not in MODES:
         raise ValueError(f"unsupported relevance_mode: {mode}")
+    if sketch.dim() != 3:
+        raise ValueError("sketch must have shape [n_pages, sketch_rows, head_dim]")
     n, S, hd = (int(x) for x in sketch.shape)
+    for name, t in (("minima", minima), ("maxima", maxima)):
+        if tuple(t.shape) != (n, hd) or t.dtype != torch.float32 or t.device != sketch.device:
+            raise ValueError(f"{name} must be fp32 [n_pages, head_dim] on the sketch's device")
+    if sketch.dtype != torch.float32:
+        raise ValueError("sketch must be fp32")
+    sketch, minima, maxima = sketch.contiguous(), minima.contiguous(), maxima.contiguous()
     q = torch.as_tensor(np.asarray(query, dtype=np.float32) if not isinstance(query, torch.Tensor) else query,
                         dtype=torch.float32, device=sketch.device).reshape(-1).contiguous()
     if q.numel() != hd:
@@ -154,6 +162,11 @@ def select_top_k(scores, candidate: np.ndarray, k: int) -> np.ndarray:
     ``session_runtime.py:425-436``)."""
     torch = _torch()
     n = int(scores.numel())
+    candidate = np.asarray(candidate)
+    if candidate.shape != (n,):
+        raise ValueError(f"candidate mask must have one entry per score ({n}), got shape {candidate.shape}")
+    if scores.dtype != torch.float32 or not scores.is_contiguous():
+        raise ValueError("scores must be a contiguous fp32 tensor")
     cand = torch.from_numpy(np.ascontiguousarray(candidate, dtype=np.uint8)).to(scores.device)
     sel = torch.empty(n, dtype=torch.uint8, device=scores.device)
     st = _lib.lib().dc_select_top_k(C.c_void_p(scores.data_ptr()), C.c_void_p(cand.data_ptr()), n, int(k),

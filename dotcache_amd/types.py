@@ -4,9 +4,11 @@ Same contract as reference ``dotcache/types.py:15-112``: the 20-field
 :class:`PageHeader` serialised as sorted-key JSON, and :class:`EncodedPage`
 holding host numpy arrays -- payload ``[G, T, W]`` uint32 (group_major),
 scales / bias ``[T, G]`` fp16, escape rows ``[T, head_dim]`` -- with the same
-byte accounting.  Pages built by this package carry no runtime sketch /
-envelope arrays (the reference builds them only for its approximate
-execution shortlist, ``dotcache/encode.py:64-75``).
+byte accounting.  ``EncodedPage`` also carries the optional runtime
+shortlist metadata of the raw rows (fp16 mean, chunk-mean sketch, min, max;
+reference ``dotcache/encode.py:64-75``): ``encode.encode_page`` builds it by
+default, as the reference does, and pages read back from a device pool have
+none.
 """
 from __future__ import annotations
 

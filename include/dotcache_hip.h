@@ -172,6 +172,29 @@ int dc_mix_pages(dc_pool pool, const int32_t* page_ids, const int32_t* token_off
                  const float* weights, int32_t n_queries, int64_t weights_stride, float* out,
                  int32_t accumulate, dc_stream_t stream);
 
+/* Grouped forms of dc_score_pages / dc_mix_pages: one launch for G groups
+ * of pages, each with its own n_queries queries, as the batched grouped
+ * decode that returns logits needs (reference
+ * dotcache/backends/torch_mps.py:4110-4273, behind
+ * dotcache/backends/torch_cuda.py:115-145,
+ * decode_grouped_multiquery_step(_prepared)_cuda_tensor).
+ *   score: page i is scored against queries[page_group[i]] (device fp32
+ *          [n_groups][n_queries][head_dim]) into logits rows
+ *          page_group[i] * n_queries + q (row stride logits_stride) at
+ *          columns token_offsets[i] + t, offsets counted within the group;
+ *   mix:   out[g * n_queries + q, :] (+)= sum over pages
+ *          [group_pages[g], group_pages[g + 1]) of weights row
+ *          g * n_queries + q times the page's values; group_pages is device
+ *          int32 [n_groups + 1]. */
+int dc_score_pages_grouped(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets,
+                           const int32_t* page_group, int32_t n_groups, int32_t n_pages, const float* queries,
+                           int32_t n_queries, float* logits, int64_t logits_stride, dc_stream_t stream);
+
+int dc_mix_pages_grouped(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets,
+                         const int32_t* group_pages, int32_t n_groups, int32_t n_pages, const float* weights,
+                         int32_t n_queries, int64_t weights_stride, float* out, int32_t accumulate,
+                         dc_stream_t stream);
+
 /* In-place row softmax exp(x - max) / sum of x[r, :n_cols] (row stride
  * `stride`), the global softmax of reference
  * dotcache/attention_reference.py:27-31 used by the decode_step entry
