@@ -423,14 +423,14 @@ def decode_grouped_multiquery_step_prepared_hip_tensor(query_groups, key_pages_b
     if len(set(totals)) != 1:
         raise ValueError("all query groups must have the same query count and token count for batched grouped decode")
     T = totals[0]
-    # token offsets within each group, the group of every page
-    offsets = np.zeros(len(kids) + 1, dtype=np.int32)
+    # first token of every page within its group, the group of every page
+    starts = np.zeros(len(kids), dtype=np.int32)
     for g in range(G):
         seg = ktok[bounds[g]:bounds[g + 1]]
-        offsets[bounds[g] + 1:bounds[g + 1] + 1] = np.cumsum(seg)
+        starts[bounds[g]:bounds[g + 1]] = np.cumsum(seg) - seg
     page_group = np.repeat(np.arange(G, dtype=np.int32), counts)
     kids_d, vids_d = torch.from_numpy(kids).to(dev), torch.from_numpy(vids).to(dev)
-    off_d = torch.from_numpy(offsets[:-1].copy()).to(dev)
+    off_d = torch.from_numpy(starts).to(dev)
     grp_d = torch.from_numpy(page_group).to(dev)
     gp_d = torch.from_numpy(bounds.astype(np.int32)).to(dev)
     logits = torch.empty((G, Q, T), dtype=torch.float32, device=dev)
