@@ -15,7 +15,8 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libdotcache_hip.so"
-SOURCES = ["dc_abi.cpp", "dc_encode.hip", "dc_score_mix.hip", "dc_decode.hip", "dc_decode_mfma.hip", "dc_shortlist.hip"]
+SOURCES = ["dc_abi.cpp", "dc_encode.hip", "dc_score_mix.hip", "dc_decode.hip", "dc_decode_mfma.hip", "dc_shortlist.hip",
+           "dc_decode_noalloc.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 anywhere in the device code.
 # -ffp-contract=off: no fused multiply-add, so the encoder's fp32 steps round

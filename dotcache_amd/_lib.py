@@ -78,6 +78,10 @@ SIGNATURES = {
                                   C.c_void_p, C.c_int32, C.c_float, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                   C.c_void_p, C.c_int64, C.c_void_p]),
     "dc_decode_workspace_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32]),
+    "dc_decode_paged_noalloc": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
+                                          C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_float,
+                                          C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
+    "dc_decode_noalloc_scratch_bytes": (C.c_int64, []),
     "dc_set_decode_path": (C.c_int, [C.c_int32]),
     "dc_lse_merge": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                C.c_void_p, C.c_void_p]),

@@ -280,6 +280,26 @@ int64_t dc_decode_workspace_bytes(int32_t n_partials, int32_t n_q, int32_t head_
 int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const void* workspace, int64_t workspace_bytes,
                  int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, int32_t head_dim, float* out, dc_stream_t stream);
 
+/* dc_decode_paged without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * The split-K partials go to a static device array of
+ * dc_decode_noalloc_scratch_bytes() bytes (32 MiB) that each GPU the library
+ * runs on holds until the process ends; n_partials (from dc_plan_decode) must
+ * fit it: n_partials * n_q * (head_dim + 2) * 4 bytes, or the call fails with
+ * DC_ESPACE.  The call allocates nothing (its first call on a device looks
+ * up that device's array).  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (concurrent streams, threads) race.  All
+ * other arguments and results are as for dc_decode_paged. */
+int dc_decode_paged_noalloc(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table,
+                            int32_t table_stride, const dc_work_item* items, int32_t n_items,
+                            const dc_merge_item* merges, int32_t n_merges, int32_t n_partials,
+                            const void* queries, int32_t queries_dtype, float query_scale, int32_t n_seqs,
+                            int32_t n_kv_heads, int32_t n_q, float* out, dc_stream_t stream);
+
+/* Bytes of the static scratch array dc_decode_paged_noalloc uses (host only). */
+int64_t dc_decode_noalloc_scratch_bytes(void);
+
 /* Process-wide decode kernel choice: 0 (default) runs the MFMA kernel when
  * every page format (M3 fp16 keys and values, M0 4- or 8-bit keys of group
  * 32, M0 4- or 8-bit values of group 32 or 64), head_dim (64/128/256) and
