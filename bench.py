@@ -53,6 +53,10 @@ def parse():
                     help="only time the execution shortlist kernels: relevance of N pages (4-row sketches, "
                          "head_dim 128) and the top-k of one min(N, 2048)-page stream; prints its own JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--encode-probe", action="store_true",
+                    help="only time the bulk page encode (dc_encode_rows_kv) of one C3 layer: the keys of 8 x 16384 "
+                         "tokens x 4 KV heads into M3 fp16 pages and the values into M0 symmetric int4 g32 pages; "
+                         "prints its own JSON line")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy a BYTES-sized device buffer three times and exit: the known-size "
                          "transfer that calibrates the FETCH_SIZE / WRITE_SIZE counters")
@@ -127,6 +131,57 @@ def shortlist_probe(n_pages: int, steps: int) -> None:
                       "unit": "pages/s", "relevance_us": out["relevance"], "relevance_bytes": nbytes,
                       "relevance_hbm_frac": nbytes / (out["relevance"] * 1e-6) / (HBM_PEAK_GBPS * 1e9),
                       "top_k_us": out["top_k"], "top_k_pages": n_tk, "k": k, "steps": steps}), flush=True)
+
+
+def encode_probe(steps: int) -> None:
+    """Bulk encode of one C3 layer in one dc_encode_rows_kv launch: 524,288
+    fp32 key rows into M3 fp16 pages and as many value rows into M0 symmetric
+    4-bit group-32 pages (head_dim 128, 64-token pages), timed over
+    ``steps`` launches between events.  Bytes per row: the 512-byte fp32 row
+    read, plus the page bytes written (256 for the key, 64 code bytes and
+    8 scale bytes for the value)."""
+    import torch
+
+    from dotcache_amd import _lib
+    from dotcache_amd.page_pool import DevicePagePool, PoolGeometry
+
+    dev = torch.device("cuda", 0)
+    B, H, T, hd, P = 8, 4, 16384, 128, 64
+    n = B * H * T
+    g = torch.Generator(device=dev).manual_seed(0)
+    k = torch.randn((n, hd), device=dev, generator=g)
+    v = torch.randn((n, hd), device=dev, generator=g)
+    kp = DevicePagePool(PoolGeometry(hd, 32, P), device=dev, reserve_bytes=n // P * 16384 + (1 << 20),
+                        reserve_pages=n // P + 16)
+    vp = DevicePagePool(PoolGeometry(hd, 32, P), device=dev, reserve_bytes=n // P * 4608 + (1 << 20),
+                        reserve_pages=n // P + 16)
+    kid = kp.allocate(_lib.FMT_M3_F16, 0, n // P, tokens=P)
+    vid = vp.allocate(_lib.FMT_M0_SYMMETRIC, 4, n // P, tokens=P)
+    rows = torch.arange(n, device=dev, dtype=torch.int64)
+    kpage = torch.from_numpy(kid).to(dev)[rows // P].contiguous()
+    vpage = torch.from_numpy(vid).to(dev)[rows // P].contiguous()
+    slots = (rows % P).to(torch.int32).contiguous()
+
+    def run():
+        kp.encode_rows_with(vp, k, v, kpage, slots, vpage, slots)
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
+        run()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    us = np.array([ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(steps)])
+    nbytes = n * (512 + 256) + n * (512 + 64 + 8)
+    mean = float(us.mean())
+    print(json.dumps({"metric": "bulk page encode (dc_encode_rows_kv, one C3 layer)", "value": 2 * n / (mean * 1e-6),
+                      "unit": "rows/s", "launch_us": mean, "launch_us_median": float(np.median(us)),
+                      "rows": 2 * n, "bytes_per_launch": nbytes,
+                      "hbm_gbps": nbytes / (mean * 1e-6) / 1e9,
+                      "hbm_frac": nbytes / (mean * 1e-6) / (HBM_PEAK_GBPS * 1e9), "steps": steps}), flush=True)
 
 
 def copy_probe(nbytes: int) -> None:
@@ -230,6 +285,9 @@ def main():
         return
     if args.shortlist_pages:
         shortlist_probe(args.shortlist_pages, max(args.steps, 1))
+        return
+    if args.encode_probe:
+        encode_probe(max(args.steps, 1))
         return
 
     from dotcache_amd.decode import set_decode_path

@@ -60,6 +60,9 @@ SIGNATURES = {
     "dc_page_blob_bytes": (C.c_int64, [C.c_int32, C.c_int32, PageGeometry]),
     "dc_page_read_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32, PageGeometry]),
     "dc_encode_rows": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, Pool, C.c_void_p]),
+    "dc_encode_rows_kv": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
+                                    C.c_void_p, C.c_void_p, Pool, Pool, C.c_void_p]),
+    "dc_set_encode_path": (C.c_int, [C.c_int32]),
     "dc_score_pages": (C.c_int, [Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_int64, C.c_void_p]),
     "dc_mix_pages": (C.c_int, [Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int64, C.c_void_p, C.c_int32, C.c_void_p]),
     "dc_score_pages_grouped": (C.c_int, [Pool, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,

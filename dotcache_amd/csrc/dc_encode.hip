@@ -1,14 +1,23 @@
 // M0 / M3 page encode and token append (gfx950).
 //
-// One thread per (row, group): min/max (or max |x|) over the group's
-// channels, the fp32 scale, round-half-even codes, and little-endian packing
-// straight into the page blob.  Bit-exact with reference
-// dotcache/modes/m0_affine.py:15-53 + dotcache/packing.py:14-48 +
-// dotcache/encode.py:399-445: every step is one IEEE fp32 operation
-// (subtract, correctly rounded divide, max), rintf rounds half to even like
-// np.round, and scales / biases are rounded to fp16 with RNE after the codes
-// were computed from the fp32 scale.  This file is compiled with
-// -ffp-contract=off so no step is fused.
+// Bit-exact with reference dotcache/modes/m0_affine.py:15-53 +
+// dotcache/packing.py:14-48 + dotcache/encode.py:399-445: every step is one
+// IEEE fp32 operation (subtract, correctly rounded divide, max), rintf
+// rounds half to even like np.round, and scales / biases are rounded to fp16
+// with RNE after the codes were computed from the fp32 scale.  This file is
+// compiled with -ffp-contract=off so no step is fused.
+//
+// Two kernels:
+//   encode_rows8_kernel (the fast path): 8 consecutive channels per lane,
+//     a row on head_dim / 8 lanes and several rows per wavefront.  A lane
+//     loads its channels with 16-byte loads, a group's min / max / max |x|
+//     is a butterfly over the group's lanes, and a lane's 8 codes are one
+//     word at 4 bits and two at 8 bits, stored as they are; 2- and 3-bit
+//     words (which lanes share) are OR-ed together in LDS.  Taken when the
+//     group size and head_dim are multiples of 8 and the padded head_dim / 8
+//     and group size / 8 are powers of two (every configuration here).
+//   encode_rows_kernel (the general path): one thread per (row, group),
+//     for any other geometry.
 #include "dc_common.h"
 
 namespace dc {
@@ -114,7 +123,290 @@ __global__ void __launch_bounds__(256) encode_rows_kernel(const void* __restrict
   }
 }
 
+// ---- fast path ---------------------------------------------------------
+
+// One encode job: rows of `values` into (row_page[r], row_slot[r]) of `pool`.
+struct EncodeJob {
+  const void* values;
+  const int32_t* row_page;
+  const int32_t* row_slot;
+  dc_pool pool;
+};
+
+constexpr int kEncThreads = 256;
+// LDS words per wavefront for 2- / 3-bit packing
+constexpr int kPackWords = 64;
+
+__device__ __forceinline__ float seg_min(float v, int lanes) {
+  for (int o = 1; o < lanes; o <<= 1) v = fminf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float seg_max(float v, int lanes) {
+  for (int o = 1; o < lanes; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Eight consecutive values of row r from channel c0 (dtype DC_F32 / F16 /
+// BF16); vec: the row start is 16-byte aligned for this dtype.
+__device__ __forceinline__ void load8(const void* values, int32_t dtype, int64_t off, bool vec, float* x) {
+  if (dtype == DC_F32) {
+    const float* p = reinterpret_cast<const float*>(values) + off;
+    if (vec) {
+      const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+      return;
+    }
+  } else if (vec) {
+    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(values) + off);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (dtype == DC_F16) {
+        x[2 * i] = __half2float(__ushort_as_half(uint16_t(w[i] & 0xffffu)));
+        x[2 * i + 1] = __half2float(__ushort_as_half(uint16_t(w[i] >> 16)));
+      } else {
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = load_value(values, dtype, off + i);
+}
+
+// blockIdx.y selects the job (K rows, V rows).  Row r of the job is handled
+// by lanes [lpr * (r % rpw), ...) of wavefront r / rpw, lpr = padded
+// head_dim / 8 lanes per row, rpw = 64 / lpr rows per wavefront.
+__global__ void __launch_bounds__(kEncThreads) encode_rows8_kernel(EncodeJob j0, EncodeJob j1, int32_t dtype,
+                                                                   int64_t n_rows, int64_t row_stride, int32_t vec,
+                                                                   int32_t lds_pack) {
+  __shared__ uint32_t pack[kEncThreads / 64][kPackWords];
+  const EncodeJob J = blockIdx.y == 0 ? j0 : j1;
+  const dc_page_geometry geo = J.pool.geometry;
+  const int32_t hd = geo.head_dim, gs = geo.group_size, C = geo.page_capacity;
+  const int32_t G = (hd + gs - 1) / gs, Gp = G * gs;
+  const int lpr = Gp / 8, lpg = gs / 8, rpw = 64 / lpr;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane % lpr, rw = lane / lpr;  // lane within its row, row within the wavefront
+  const int64_t r = (int64_t(blockIdx.x) * (kEncThreads / 64) + wave) * rpw + rw;
+  const int32_t c0 = 8 * q, g = c0 / gs, li = (c0 - g * gs) / 8;
+
+  // the row's page and slot; rows that do not exist or name no valid
+  // destination stay idle (they still reach the block barriers)
+  bool live = rw < rpw && r < n_rows;
+  dc_page_desc d{};
+  int32_t t = 0;
+  BlobLayout L{};
+  uint8_t* blob = nullptr;
+  if (live) {
+    const int32_t pid = J.row_page[r];
+    t = J.row_slot[r];
+    live = pid >= 0 && pid < J.pool.n_descs && t >= 0 && t < C;
+    if (live) {
+      d = J.pool.descs[pid];
+      L = blob_layout(d.format, d.bits, geo);
+      live = (int64_t(d.block) << 8) + L.total <= J.pool.arena_bytes;
+      blob = reinterpret_cast<uint8_t*>(J.pool.arena) + (uint64_t(d.block) << 8);
+    }
+  }
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = 0.f;
+  if (live && c0 < hd) load8(J.values, dtype, r * row_stride + c0, vec != 0, x);  // channels past hd: zero padding
+
+  const bool m0 = live && is_m0(d.format);
+  uint32_t w0 = 0, w1 = 0;  // this lane's code bits (8 codes, little-endian)
+  int bits = d.bits;
+  if (m0) {
+    float lo = x[0], hi = x[0], am = fabsf(x[0]);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      lo = fminf(lo, x[i]);
+      hi = fmaxf(hi, x[i]);
+      am = fmaxf(am, fabsf(x[i]));
+    }
+    lo = seg_min(lo, lpg);
+    hi = seg_max(hi, lpg);
+    am = seg_max(am, lpg);
+    const uint32_t top = (1u << bits) - 1u;
+    const bool affine = d.format == DC_FMT_M0_AFFINE;
+    const int32_t qmax = (1 << (bits - 1)) - 1;
+    const float scale = affine ? fmaxf((hi - lo) / float(top), 1e-8f) : fmaxf(am / float(qmax > 1 ? qmax : 1), 1e-8f);
+    uint64_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t code;
+      if (affine) {
+        const float qv = rintf((x[i] - lo) / scale);
+        code = uint32_t(fminf(fmaxf(qv, 0.f), float(top)));
+      } else {
+        const float qv = fminf(fmaxf(rintf(x[i] / scale), -float(qmax)), float(qmax));
+        const int32_t sc = int32_t(qv) + qmax;
+        code = uint32_t(sc < 0 ? 0 : (sc > int32_t(top) ? int32_t(top) : sc));
+      }
+      acc |= uint64_t(code) << (i * bits);
+    }
+    w0 = uint32_t(acc);
+    w1 = uint32_t(acc >> 32);
+    uint32_t* payload = reinterpret_cast<uint32_t*>(blob);
+    const int64_t wb = geo.layout == 0 ? (int64_t(g) * C + t) * L.words : (int64_t(t) * G + g) * L.words;
+    if (bits == 4) {
+      payload[wb + li] = w0;
+    } else if (bits == 8) {
+      *reinterpret_cast<uint2*>(payload + wb + 2 * li) = uint2{w0, w1};
+    }
+    if (li == 0) {
+      reinterpret_cast<__half*>(blob + L.scales_off)[t * G + g] = __float2half_rn(scale);
+      if (affine) reinterpret_cast<__half*>(blob + L.bias_off)[t * G + g] = __float2half_rn(lo);
+    }
+  } else if (live && c0 < hd) {
+    const int64_t e = int64_t(t) * hd + c0;
+    if (d.format == DC_FMT_M3_F16) {
+      uint32_t h[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        h[i] = uint32_t(__half_as_ushort(__float2half_rn(x[2 * i]))) |
+               (uint32_t(__half_as_ushort(__float2half_rn(x[2 * i + 1]))) << 16);
+      *reinterpret_cast<uint4*>(reinterpret_cast<__half*>(blob) + e) = uint4{h[0], h[1], h[2], h[3]};
+    } else if (d.format == DC_FMT_M3_F32) {
+      float* o = reinterpret_cast<float*>(blob) + e;
+      *reinterpret_cast<float4*>(o) = float4{x[0], x[1], x[2], x[3]};
+      *reinterpret_cast<float4*>(o + 4) = float4{x[4], x[5], x[6], x[7]};
+    }
+  }
+  if (live && d.format == DC_FMT_M3_I8) {  // one fp16 scale for the whole row
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(x[i]));
+    am = seg_max(am, lpr);
+    const __half s16 = __float2half_rn(fmaxf(am / 127.0f, 1e-8f));
+    const float sv = __half2float(s16);
+    if (c0 < hd) {
+      uint32_t b[2] = {0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float qv = fminf(fmaxf(rintf(x[i] / sv), -127.f), 127.f);
+        b[i >> 2] |= (uint32_t(int32_t(qv)) & 0xffu) << (8 * (i & 3));
+      }
+      *reinterpret_cast<uint2*>(blob + int64_t(t) * hd + c0) = uint2{b[0], b[1]};
+    }
+    if (q == 0) reinterpret_cast<__half*>(blob + L.scales_off)[t] = s16;
+  }
+  if (!lds_pack) return;  // uniform: no 2- / 3-bit pages in this launch's pools
+
+  // 2- and 3-bit codes: a lane's 8 codes (16 or 24 bits) start at bit
+  // 8 bits li of its group's words and may share words with the next lane;
+  // OR them into the wavefront's LDS words, then store whole words
+  const bool narrow = m0 && bits < 4;
+  const int wpr = G * L.words;  // words of one row (the same for every narrow row of this job)
+  for (int i = lane; i < kPackWords; i += 64) pack[wave][i] = 0u;
+  __syncthreads();
+  if (narrow) {
+    const int bit = 8 * bits * li, wi = bit >> 5, off = bit & 31;
+    uint32_t* rowp = pack[wave] + rw * wpr + g * L.words;
+    atomicOr(rowp + wi, w0 << off);
+    if (off + 8 * bits > 32) atomicOr(rowp + wi + 1, w0 >> (32 - off));
+  }
+  __syncthreads();
+  if (narrow && li == 0) {
+    uint32_t* payload = reinterpret_cast<uint32_t*>(blob);
+    const int64_t wb = geo.layout == 0 ? (int64_t(g) * C + t) * L.words : (int64_t(t) * G + g) * L.words;
+    for (int w = 0; w < L.words; ++w) payload[wb + w] = pack[wave][rw * wpr + g * L.words + w];
+  }
+}
+
+// Whether a pool's geometry fits encode_rows8_kernel: 8-channel lanes that
+// tile its groups and rows within one wavefront, and (2-/3-bit pages) the
+// wavefront's packed words within its LDS share.
+static bool fits_rows8(const dc_page_geometry& g) {
+  const int32_t G = num_groups(g), Gp = G * g.group_size;
+  auto pow2 = [](int32_t v) { return v > 0 && (v & (v - 1)) == 0; };
+  if (g.head_dim % 8 || g.group_size % 8 || !pow2(g.group_size / 8) || !pow2(Gp / 8) || Gp / 8 > 64) return false;
+  // narrow packing: rows per wavefront x words per row <= kPackWords
+  const int32_t rpw = 64 / (Gp / 8);
+  return int64_t(rpw) * G * words_per_group(g.group_size, 3) <= kPackWords;
+}
+
+static bool has_narrow(const dc_pool& p) {
+  const uint64_t narrow = (uint64_t(1) << (DC_FMT_M0_AFFINE * 9 + 2)) | (uint64_t(1) << (DC_FMT_M0_AFFINE * 9 + 3)) |
+                          (uint64_t(1) << (DC_FMT_M0_SYMMETRIC * 9 + 2)) |
+                          (uint64_t(1) << (DC_FMT_M0_SYMMETRIC * 9 + 3));
+  return p.format_mask == 0 || (p.format_mask & narrow) != 0;
+}
+
+static int g_encode_path = 0;  // 0: fast kernel where it fits; 1: general kernel only
+
+static int encode_launch(const EncodeJob* jobs, int n_jobs, int32_t dtype, int64_t n_rows, int64_t row_stride,
+                         hipStream_t stream) {
+  // the fast kernel for every job whose geometry fits it, in one launch
+  bool fast[2] = {false, false};
+  int32_t rows_per_block = 1 << 30;
+  bool vec = true, narrow = false;
+  const int esize = dtype == DC_F32 ? 4 : 2;
+  for (int i = 0; i < n_jobs; ++i) {
+    fast[i] = g_encode_path == 0 && fits_rows8(jobs[i].pool.geometry);
+    if (!fast[i]) continue;
+    const dc_page_geometry& g = jobs[i].pool.geometry;
+    const int32_t lpr = num_groups(g) * g.group_size / 8;
+    rows_per_block = rows_per_block < (kEncThreads / lpr) ? rows_per_block : kEncThreads / lpr;
+    vec = vec && (reinterpret_cast<uintptr_t>(jobs[i].values) % 16 == 0) && (row_stride * esize) % 16 == 0;
+    narrow = narrow || has_narrow(jobs[i].pool);
+  }
+  const bool all_fast = fast[0] && (n_jobs < 2 || fast[1]);
+  if (fast[0] || (n_jobs > 1 && fast[1])) {
+    const int64_t blocks = (n_rows + rows_per_block - 1) / rows_per_block;
+    if (blocks > 0x7fffffff) return fail(DC_EINVAL, "too many rows");
+    if (all_fast) {
+      hipLaunchKernelGGL(encode_rows8_kernel, dim3(uint32_t(blocks), uint32_t(n_jobs)), dim3(kEncThreads), 0, stream,
+                         jobs[0], n_jobs > 1 ? jobs[1] : jobs[0], dtype, n_rows, row_stride, int32_t(vec),
+                         int32_t(narrow));
+    } else {
+      const EncodeJob& f = fast[0] ? jobs[0] : jobs[1];
+      hipLaunchKernelGGL(encode_rows8_kernel, dim3(uint32_t(blocks), 1), dim3(kEncThreads), 0, stream, f, f, dtype,
+                         n_rows, row_stride, int32_t(vec), int32_t(narrow));
+    }
+    if (int rc = check_hip(hipGetLastError(), "encode_rows8_kernel launch")) return rc;
+  }
+  for (int i = 0; i < n_jobs; ++i) {
+    if (fast[i]) continue;
+    const int32_t G = num_groups(jobs[i].pool.geometry);
+    const int64_t blocks = (n_rows * G + 255) / 256;
+    if (blocks > 0x7fffffff) return fail(DC_EINVAL, "too many rows");
+    hipLaunchKernelGGL(encode_rows_kernel, dim3(uint32_t(blocks)), dim3(256), 0, stream, jobs[i].values, dtype, n_rows,
+                       row_stride, jobs[i].row_page, jobs[i].row_slot, jobs[i].pool, G);
+    if (int rc = check_hip(hipGetLastError(), "encode_rows_kernel launch")) return rc;
+  }
+  return DC_OK;
+}
+
+static int check_encode_args(const void* values, int32_t dtype, int64_t n_rows, int64_t row_stride,
+                             const int32_t* row_page, const int32_t* row_slot, const dc_pool& pool, const char* who) {
+  if (int rc = validate_geometry(pool.geometry)) return rc;
+  if (!values || !row_page || !row_slot || !pool.arena || !pool.descs) return fail(DC_EINVAL, "%s: null pointer", who);
+  if (row_stride < pool.geometry.head_dim) return fail(DC_EINVAL, "%s: row_stride is smaller than head_dim", who);
+  return DC_OK;
+}
+
 }  // namespace dc
+
+extern "C" int dc_encode_rows_kv(const void* k_values, const void* v_values, int32_t values_dtype, int64_t n_rows,
+                                 int64_t row_stride, const int32_t* k_row_page, const int32_t* k_row_slot,
+                                 const int32_t* v_row_page, const int32_t* v_row_slot, dc_pool k_pool, dc_pool v_pool,
+                                 dc_stream_t stream) {
+  if (n_rows < 0) return dc::fail(DC_EINVAL, "n_rows must be non-negative");
+  if (values_dtype != DC_F32 && values_dtype != DC_F16 && values_dtype != DC_BF16)
+    return dc::fail(DC_EINVAL, "values_dtype must be DC_F32, DC_F16 or DC_BF16");
+  if (n_rows == 0) return DC_OK;
+  if (int rc = dc::check_encode_args(k_values, values_dtype, n_rows, row_stride, k_row_page, k_row_slot, k_pool,
+                                     "dc_encode_rows_kv (keys)"))
+    return rc;
+  if (int rc = dc::check_encode_args(v_values, values_dtype, n_rows, row_stride, v_row_page, v_row_slot, v_pool,
+                                     "dc_encode_rows_kv (values)"))
+    return rc;
+  const dc::EncodeJob jobs[2] = {{k_values, k_row_page, k_row_slot, k_pool}, {v_values, v_row_page, v_row_slot, v_pool}};
+  return dc::encode_launch(jobs, 2, values_dtype, n_rows, row_stride, hipStream_t(stream));
+}
 
 extern "C" int dc_encode_rows(const void* values, int32_t values_dtype, int64_t n_rows, int64_t row_stride,
                               const int32_t* row_page, const int32_t* row_slot, dc_pool pool,
@@ -122,16 +414,19 @@ extern "C" int dc_encode_rows(const void* values, int32_t values_dtype, int64_t 
   if (int rc = dc::validate_geometry(pool.geometry)) return rc;
   if (n_rows < 0) return dc::fail(DC_EINVAL, "n_rows must be non-negative");
   if (n_rows == 0) return DC_OK;
-  if (!values || !row_page || !row_slot || !pool.arena || !pool.descs)
-    return dc::fail(DC_EINVAL, "dc_encode_rows: null pointer");
   if (values_dtype != DC_F32 && values_dtype != DC_F16 && values_dtype != DC_BF16)
     return dc::fail(DC_EINVAL, "values_dtype must be DC_F32, DC_F16 or DC_BF16");
-  if (row_stride < pool.geometry.head_dim) return dc::fail(DC_EINVAL, "row_stride is smaller than head_dim");
-  const int32_t G = dc::num_groups(pool.geometry);
-  const int64_t threads = n_rows * G;
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffff) return dc::fail(DC_EINVAL, "too many rows");
-  hipLaunchKernelGGL(dc::encode_rows_kernel, dim3(uint32_t(blocks)), dim3(256), 0, hipStream_t(stream), values,
-                     values_dtype, n_rows, row_stride, row_page, row_slot, pool, G);
-  return dc::check_hip(hipGetLastError(), "dc_encode_rows launch");
+  if (int rc = dc::check_encode_args(values, values_dtype, n_rows, row_stride, row_page, row_slot, pool,
+                                     "dc_encode_rows"))
+    return rc;
+  const dc::EncodeJob job{values, row_page, row_slot, pool};
+  return dc::encode_launch(&job, 1, values_dtype, n_rows, row_stride, hipStream_t(stream));
+}
+
+// Process-wide encode kernel choice (0: the fast kernel where it fits, 1:
+// the general kernel only), for cross-checking the two.
+extern "C" int dc_set_encode_path(int32_t path) {
+  if (path < 0 || path > 1) return dc::fail(DC_EINVAL, "encode path must be 0 (auto) or 1 (general)");
+  dc::g_encode_path = path;
+  return DC_OK;
 }

@@ -42,6 +42,15 @@ def _torch():
     return torch
 
 
+def set_encode_path(path: str) -> None:
+    """``"auto"`` (the wavefront encode kernel where the geometry fits it)
+    or ``"general"`` (the one-thread-per-group kernel only)."""
+    paths = {"auto": 0, "general": 1}
+    if path not in paths:
+        raise ValueError("encode path must be 'auto' or 'general'")
+    _lib.check(_lib.lib().dc_set_encode_path(paths[path]), "dc_set_encode_path")
+
+
 def page_format_of(mode: str, scheme: str, bits: int, escape_dtype: str = "float16") -> tuple[int, int]:
     """(dc_page_format, bits) for a page mode; ValueError if this backend cannot hold it."""
     if mode == "M3":
@@ -394,6 +403,30 @@ class DevicePagePool:
             C.c_void_p(slot.data_ptr()), pool, C.c_void_p(current_stream_ptr()),
         )
         _lib.check(st, "dc_encode_rows")
+
+    def encode_rows_with(self, v_pool: "DevicePagePool", k_values, v_values, k_page_ids, k_slots, v_page_ids,
+                         v_slots) -> None:
+        """Keys into this pool and values into ``v_pool`` in one launch
+        (``dc_encode_rows_kv``): the per-step append of new tokens.  Both
+        value arrays are ``[n, head_dim]`` of one dtype and row stride."""
+        torch = _torch()
+        hd = self.geometry.head_dim
+        if v_pool.geometry.head_dim != hd:
+            raise ValueError("key and value pools must share head_dim")
+        if k_values.dim() != 2 or k_values.shape[1] != hd or tuple(v_values.shape) != tuple(k_values.shape):
+            raise ValueError("key and value rows must have the same shape [n, head_dim]")
+        if k_values.dtype != v_values.dtype:
+            raise ValueError("key and value rows must have the same dtype")
+        k_values, v_values = k_values.contiguous(), v_values.contiguous()
+        n = k_values.shape[0]
+        ids = [torch.as_tensor(x, dtype=torch.int32, device=self.device).contiguous()
+               for x in (k_page_ids, k_slots, v_page_ids, v_slots)]
+        if any(t.numel() != n for t in ids):
+            raise ValueError("page_ids and slots must have one entry per row")
+        st = _lib.lib().dc_encode_rows_kv(
+            C.c_void_p(k_values.data_ptr()), C.c_void_p(v_values.data_ptr()), dtype_code(k_values), n, hd,
+            *(C.c_void_p(t.data_ptr()) for t in ids), self.c_pool(), v_pool.c_pool(), C.c_void_p(current_stream_ptr()))
+        _lib.check(st, "dc_encode_rows_kv")
 
     def read_bytes(self, page_ids) -> int:
         """Compressed bytes a reader fetches for these pages (valid tokens only)."""

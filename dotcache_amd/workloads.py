@@ -213,8 +213,8 @@ class Workload:
         """Encode this step's new K / V row of every (sequence, KV head) into
         slot 0 of its tail page (the steady-state cost of one append; the
         tail holds exactly that one token)."""
-        self.k_pool.encode_rows(self.new_k[l], self.tail_k_dev[l], self.slot_dev)
-        self.v_pool.encode_rows(self.new_v[l], self.tail_v_dev[l], self.slot_dev)
+        self.k_pool.encode_rows_with(self.v_pool, self.new_k[l], self.new_v[l], self.tail_k_dev[l], self.slot_dev,
+                                     self.tail_v_dev[l], self.slot_dev)
 
 
 def _gen(shape, gen, dist: str, device):

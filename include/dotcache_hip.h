@@ -152,6 +152,23 @@ int dc_encode_rows(const void* values, int32_t values_dtype, int64_t n_rows, int
                    const int32_t* row_slot /* device [n_rows] */,
                    dc_pool pool, dc_stream_t stream);
 
+/* The keys and values of the same new tokens in one launch: k_values rows
+ * into (k_row_page, k_row_slot) of k_pool and v_values rows into
+ * (v_row_page, v_row_slot) of v_pool, each as dc_encode_rows would (both
+ * arrays have n_rows rows of one dtype and row stride).  The per-step append
+ * of a decode writes both (reference dotcache/model_kv_cache.py:3830-3902,
+ * append_step, encoding K and V pages at :789-830). */
+int dc_encode_rows_kv(const void* k_values, const void* v_values, int32_t values_dtype, int64_t n_rows,
+                      int64_t row_stride, const int32_t* k_row_page, const int32_t* k_row_slot,
+                      const int32_t* v_row_page, const int32_t* v_row_slot, dc_pool k_pool, dc_pool v_pool,
+                      dc_stream_t stream);
+
+/* Process-wide encode kernel choice: 0 (default) runs the wavefront kernel
+ * (8 channels per lane, several rows per wavefront) wherever the pool's
+ * geometry fits it, 1 always runs the general one-thread-per-group kernel
+ * (for cross-checking the two).  Host only; not thread-safe. */
+int dc_set_encode_path(int32_t path);
+
 /* ---- read path: per-page entry points (score_page / mix_page) ------- */
 
 /* logits[q, token_offsets[i] + t] = score of query q against token t of

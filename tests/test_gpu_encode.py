@@ -135,3 +135,119 @@ def test_encode_rejects_bad_shapes():
         encode_page(np.zeros((4, 32), np.float32), cfg, kind="K")
     with pytest.raises(ValueError):
         encode_page(np.zeros((4,), np.float32), cfg, kind="K")
+
+
+# ---- the wavefront encode kernel against the general one and the oracle ----
+
+GEOMS = [  # (head_dim, group_size): the wavefront kernel's shapes and two it leaves to the general kernel
+    (128, 32), (64, 32), (256, 32), (128, 64), (48, 32), (32, 16), (128, 128), (64, 8),
+    (96, 32),   # padded head_dim / 8 = 12 lanes: general kernel
+    (40, 20),   # group of 20 channels: general kernel
+]
+FMTS = [("M0", "affine", b) for b in (2, 3, 4, 8)] + [("M0", "symmetric", b) for b in (2, 3, 4, 8)] + [
+    ("M3", "float16", 0), ("M3", "float32", 0), ("M3", "int8", 0)]
+
+
+def _encode_all(pool, fmts, x, slots):
+    """One page per format of ``fmts``; every row of x into every page at
+    ``slots``; the pages downloaded."""
+    from dotcache_amd.page_pool import page_format_of
+
+    torch = _torch()
+    out = []
+    for mode, sch, bits in fmts:
+        fmt, b = page_format_of(mode, "affine" if mode == "M3" else sch, bits or 4, sch if mode == "M3" else "float16")
+        pid = int(pool.allocate(fmt, b, 1, tokens=int(slots.max()) + 1)[0])
+        pool.encode_rows(x, np.full(len(slots), pid, np.int32), slots.astype(np.int32))
+        out.append(pool.download_page(pid))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("stride_pad", [0, 3])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("hd,gs", GEOMS)
+def test_wavefront_encode_matches_general_kernel_and_oracle(hd, gs, dtype, stride_pad):
+    """Every format, rows written to scattered slots of a 64-token page, rows
+    read through a padded stride (stride_pad 3: not 16-byte aligned, the
+    per-element load path): the wavefront kernel's blobs equal the general
+    kernel's byte for byte and the oracle's encode of the same rows."""
+    torch = _torch()
+    from dotcache_amd.page_pool import DevicePagePool, PoolGeometry, set_encode_path
+
+    rng = np.random.default_rng(hd * 100 + gs + stride_pad)
+    T = 37
+    x32 = hard_values(rng, T, hd)
+    full = torch.zeros((T, hd + stride_pad), dtype=getattr(torch, dtype))
+    full[:, :hd] = torch.from_numpy(x32).to(full.dtype)
+    x = full.cuda()[:, :hd]
+    xr = full[:, :hd].float().numpy()  # the values the encoder reads
+    slots = rng.permutation(64)[:T]
+    res = {}
+    for path in ("auto", "general"):
+        set_encode_path(path)
+        try:
+            pool = DevicePagePool(PoolGeometry(hd, gs, 64), reserve_bytes=1 << 22)
+            res[path] = _encode_all(pool, FMTS, x, slots)
+        finally:
+            set_encode_path("auto")
+    order = np.argsort(slots)
+    for (mode, sch, bits), a, b in zip(FMTS, res["auto"], res["general"]):
+        for name in ("payload", "scales", "bias", "escape_payload", "escape_scales"):
+            u, v = getattr(a, name), getattr(b, name)
+            assert (u is None) == (v is None), name
+            if u is not None:
+                np.testing.assert_array_equal(u.view(np.uint8), v.view(np.uint8), err_msg=f"{mode}/{sch}/{bits} {name}")
+        # the oracle on the rows in slot order (slots past the rows are never read back)
+        want = O.encode_page(xr[order], head_dim=hd, group_size=gs, kind="K", mode=mode,
+                             scheme="affine" if mode == "M3" else sch, bits=bits or 4,
+                             escape_dtype=sch if mode == "M3" else "float16")
+        rows = np.sort(slots)
+        if mode == "M0":
+            got_codes = a.payload if a.header.layout == "group_major" else None
+            np.testing.assert_array_equal(got_codes[:, rows], want.payload, err_msg=f"{mode}/{sch}/{bits} codes")
+            np.testing.assert_array_equal(a.scales[rows].view(np.uint16), want.scales.view(np.uint16))
+            if want.bias is not None:
+                np.testing.assert_array_equal(a.bias[rows].view(np.uint16), want.bias.view(np.uint16))
+        else:
+            np.testing.assert_array_equal(a.escape_payload[rows].view(np.uint8), want.escape_payload.view(np.uint8))
+            if want.escape_scales is not None:
+                np.testing.assert_array_equal(a.escape_scales[rows].view(np.uint16), want.escape_scales.view(np.uint16))
+
+
+def test_encode_rows_kv_equals_two_calls():
+    """dc_encode_rows_kv (keys and values in one launch, different pools,
+    value group 64) writes exactly what two dc_encode_rows calls write."""
+    torch = _torch()
+    from dotcache_amd import _lib
+    from dotcache_amd.page_pool import DevicePagePool, PoolGeometry
+
+    rng = np.random.default_rng(31)
+    n, hd = 24, 128
+    k = torch.from_numpy(hard_values(rng, n, hd)).cuda()
+    v = torch.from_numpy(hard_values(rng, n, hd)).cuda()
+    slots = np.tile(rng.permutation(64)[: n // 2], 2).astype(np.int32)
+    pages = {}
+    for tag in ("one", "two"):
+        kp = DevicePagePool(PoolGeometry(hd, 32, 64), reserve_bytes=1 << 20)
+        vp = DevicePagePool(PoolGeometry(hd, 64, 64), reserve_bytes=1 << 20)
+        kid = np.concatenate([kp.allocate(_lib.FMT_M3_F16, 0, 1, tokens=64),
+                              kp.allocate(_lib.FMT_M0_AFFINE, 4, 1, tokens=64)])
+        vid = vp.allocate(_lib.FMT_M0_SYMMETRIC, 8, 2, tokens=64)
+        kpage, vpage = np.repeat(kid, n // 2).astype(np.int32), np.repeat(vid, n // 2).astype(np.int32)
+        if tag == "one":
+            kp.encode_rows_with(vp, k, v, kpage, slots, vpage, slots)
+        else:
+            kp.encode_rows(k, kpage, slots)
+            vp.encode_rows(v, vpage, slots)
+        torch.cuda.synchronize()
+        pages[tag] = [kp.download_page(int(i), kind="K") for i in kid] + [vp.download_page(int(i), kind="V") for i in vid]
+    rows = np.sort(slots[: n // 2])
+    for a, b in zip(pages["one"], pages["two"]):
+        for name in ("payload", "scales", "bias", "escape_payload"):
+            u, w = getattr(a, name), getattr(b, name)
+            assert (u is None) == (w is None), name
+            if u is not None:
+                axis = 1 if name == "payload" else 0
+                np.testing.assert_array_equal(np.take(u, rows, axis=axis).view(np.uint8),
+                                              np.take(w, rows, axis=axis).view(np.uint8), err_msg=name)
