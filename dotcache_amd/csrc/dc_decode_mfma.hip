@@ -64,17 +64,18 @@ __device__ __forceinline__ h2 h2_of(uint32_t v) { return __builtin_bit_cast(h2, 
 // fp16 pair (lo, hi) from two floats, round to nearest even.
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) { return bits_of(h2{(_Float16)lo, (_Float16)hi}); }
 
-// Two fp32 values as their fp16 high parts rtz(x) and fp16 residuals
-// rtz(x - rtz(x)); x - rtz(x) is exact in fp32, so the pair carries x to
-// about 2^-22 relative.  neg1 is -1 held in a register the compiler cannot
-// see through, so x - hi stays one fma with an fp16 operand (v_fma_mix_f32).
+// The products a0 * b0 and a1 * b1 (fp32 times fp16-exact values) as fp16
+// pairs: high parts hi = rne16(a b) and residuals rne16(a b - hi), each one
+// mixed-precision fma that writes an fp16 half (v_fma_mix_lo/hi_f16, a
+// single rounding of the exact a b or a b - hi).  The pair carries a b to
+// about 2^-22 relative while hi and the residual stay in fp16's normal range.
 struct Split2 {
   uint32_t hi, res;
 };
-__device__ __forceinline__ Split2 split2(float x0, float x1, float neg1) {
-  const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-  const float r0 = __builtin_fmaf(neg1, float(hi[0]), x0), r1 = __builtin_fmaf(neg1, float(hi[1]), x1);
-  return {bits_of(hi), __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1))};
+__device__ __forceinline__ Split2 split_products(float a0, float b0, float a1, float b1) {
+  const _Float16 h0 = (_Float16)__builtin_fmaf(a0, b0, 0.f), h1 = (_Float16)__builtin_fmaf(a1, b1, 0.f);
+  const _Float16 l0 = (_Float16)__builtin_fmaf(a0, b0, -float(h0)), l1 = (_Float16)__builtin_fmaf(a1, b1, -float(h1));
+  return {bits_of(h2{h0, h1}), bits_of(h2{l0, l1})};
 }
 
 // Weights are exp2(logit - m_ref), with m_ref the head's running max when it
@@ -317,8 +318,6 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
   for (int g = 0; g < VG; ++g) bsum[g] = 0.f;
   float m_ref = -INFINITY, l_part = 0.f;
-  float neg1 = -1.f;
-  asm volatile("" : "+v"(neg1));
   // the fp16 magic 0x6400 pair, held in a VGPR the compiler cannot see
   // through: (w & mask) | magic with a scalar mask is then one v_and_or_b32
   // (a VOP3 here takes no literal and at most one scalar operand)
@@ -655,10 +654,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
           const int e0 = (2 * pp) * VG + g, e1 = (2 * pp + 1) * VG + g;  // (token, group) entries
-          // weight x fp16 scale as an fma with a zero addend: one v_fma_mix_f32
-          const float x0 = __builtin_fmaf(pw[2 * pp], float(h2_of(sw[e0 >> 1])[e0 & 1]), 0.f);
-          const float x1 = __builtin_fmaf(pw[2 * pp + 1], float(h2_of(sw[e1 >> 1])[e1 & 1]), 0.f);
-          const Split2 sp = split2(x0, x1, neg1);
+          // weight x fp16 scale straight to fp16 high and residual parts
+          const Split2 sp = split_products(pw[2 * pp], float(h2_of(sw[e0 >> 1])[e0 & 1]), pw[2 * pp + 1],
+                                           float(h2_of(sw[e1 >> 1])[e1 & 1]));
           fa_hi.u[pp] = sp.hi;
           fa_res.u[pp] = sp.res;
           if constexpr (VAFF) {  // fp16 bias times weight: one v_fma_mix_f32 each
@@ -692,7 +690,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       Frag fa_hi, fa_res;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
-        const Split2 sp = split2(kVS * pa[2 * pp], kVS * pa[2 * pp + 1], neg1);
+        const Split2 sp = split_products(pa[2 * pp], kVS, pa[2 * pp + 1], kVS);
         fa_hi.u[pp] = sp.hi;
         fa_res.u[pp] = sp.res;
       }

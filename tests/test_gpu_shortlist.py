@@ -175,3 +175,27 @@ def test_encode_page_stores_the_reference_runtime_metadata():
         assert page.runtime_page_sketch.shape == (min(4, t), 32)
     bare = encode_page(x, cfg, kind="K", build_runtime_metadata=False)
     assert bare.runtime_page_sketch is None and bare.runtime_page_mean is None
+
+
+def test_select_top_k_across_tiles_with_ties():
+    """Top-k over more than two LDS tiles of the kernel (4096 scores each) and
+    a last tile that is not a multiple of 16, with equal scores on both sides
+    of the tile boundaries: the selected set is Python's stable
+    sorted(..., reverse=True)[:k] over the candidates."""
+    import torch
+
+    from dotcache_amd.shortlist import select_top_k
+
+    rng = np.random.default_rng(77)
+    n = 2 * 4096 + 37
+    s = rng.integers(0, 40, size=n).astype(np.float32)  # many ties everywhere
+    for b in (4096, 8192):
+        s[b - 3: b + 3] = 17.0  # equal scores straddling each tile boundary
+    s[-5:] = 39.0
+    cand = rng.random(n) < 0.6
+    cand[[4095, 4096, 8191, 8192]] = True
+    got_scores = torch.from_numpy(s).cuda()
+    for k in (1, 150, 700, int(cand.sum()), int(cand.sum()) + 5):
+        order = sorted(np.flatnonzero(cand).tolist(), key=lambda i: s[i], reverse=True)
+        want = sorted(order[:k])
+        assert np.flatnonzero(select_top_k(got_scores, cand, k)).tolist() == want, k
