@@ -463,44 +463,44 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
   auto score_chunk = [&](const PageMeta& m, const Regs& R, const uint32_t* lds, auto kbi, float* Ls) __attribute__((always_inline)) {
     const uint32_t* kl = kbuf(kbi);
+    // MFMA results are read a few instructions after issue only at the very
+    // end: the M3 paths keep four independent accumulation chains (token
+    // tile hh x high / residual query part), the M0 path scales group g - 1
+    // while the MFMAs of group g run
     if (key_is_m3(m)) {
-      if constexpr (kDmaK) {
+      if constexpr (kDmaK || !Regs::kWordKeys) {
+        f32x4 dh[2], dl[2];
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          f32x4 d = {0.f, 0.f, 0.f, 0.f};
+        for (int hh = 0; hh < 2; ++hh) dh[hh] = dl[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int g = 0; g < KG; ++g) {
-            const u32x4 x = *reinterpret_cast<const u32x4*>(kl + krd[hh][g]);
-            Frag ka;
-            ka.u[0] = x.x; ka.u[1] = x.y; ka.u[2] = x.z; ka.u[3] = x.w;
-            d = mfma(ka, qhi[g], d);
-            d = mfma(ka, qlo[g], d);
-          }
+        for (int g = 0; g < KG; ++g) {
+          Frag ka[2];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = d[i];
-        }
-      } else if constexpr (!Regs::kWordKeys) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int g = 0; g < KG; ++g) {
-            Frag ka;
-            const u32x4 x = R.kr[hh][g];  // channels (0, 1), (2, 3), (4, 5), (6, 7)
-            if constexpr (kPairedQ) {        // -> (0, 4), (1, 5), (2, 6), (3, 7)
-              ka.u[0] = __builtin_amdgcn_perm(x.z, x.x, 0x05040100u);
-              ka.u[1] = __builtin_amdgcn_perm(x.z, x.x, 0x07060302u);
-              ka.u[2] = __builtin_amdgcn_perm(x.w, x.y, 0x05040100u);
-              ka.u[3] = __builtin_amdgcn_perm(x.w, x.y, 0x07060302u);
+          for (int hh = 0; hh < 2; ++hh) {
+            if constexpr (kDmaK) {
+              const u32x4 x = *reinterpret_cast<const u32x4*>(kl + krd[hh][g]);
+              ka[hh].u[0] = x.x; ka[hh].u[1] = x.y; ka[hh].u[2] = x.z; ka[hh].u[3] = x.w;
             } else {
-              ka.u[0] = x.x; ka.u[1] = x.y; ka.u[2] = x.z; ka.u[3] = x.w;
+              const u32x4 x = R.kr[hh][g];  // channels (0, 1), (2, 3), (4, 5), (6, 7)
+              if constexpr (kPairedQ) {        // -> (0, 4), (1, 5), (2, 6), (3, 7)
+                ka[hh].u[0] = __builtin_amdgcn_perm(x.z, x.x, 0x05040100u);
+                ka[hh].u[1] = __builtin_amdgcn_perm(x.z, x.x, 0x07060302u);
+                ka[hh].u[2] = __builtin_amdgcn_perm(x.w, x.y, 0x05040100u);
+                ka[hh].u[3] = __builtin_amdgcn_perm(x.w, x.y, 0x07060302u);
+              } else {
+                ka[hh].u[0] = x.x; ka[hh].u[1] = x.y; ka[hh].u[2] = x.z; ka[hh].u[3] = x.w;
+              }
             }
-            d = mfma(ka, qhi[g], d);
-            d = mfma(ka, qlo[g], d);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = d[i];
+          for (int hh = 0; hh < 2; ++hh) dh[hh] = mfma(ka[hh], qhi[g], dh[hh]);
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) dl[hh] = mfma(ka[hh], qlo[g], dl[hh]);
         }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = dh[hh][i] + dl[hh][i];
       }
     } else if constexpr (KMODE != KEYS_M3) {  // M0 4- or 8-bit, group 32: scale and bias per group in fp32
       // affine: codes n, bias b; symmetric: codes n - (2^(KBITS-1) - 1), no
@@ -515,23 +515,43 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       const h2 kadd0 = {(_Float16)(-1024.f - zp), (_Float16)(-1024.f - zp)};
       const h2 kadd1 = {(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)};
       const h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+      // scales / biases of the D-row tokens 8 kb + 4 hh + i, all groups: [4][KG] fp16 per tile
+      uint32_t sw[2][2 * KG], bw[2][2 * KG];
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        // scales / biases of the D-row tokens 8 kb + 4 hh + i, all groups: [4][KG] fp16
-        uint32_t sw[2 * KG], bw[2 * KG];
+      for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int k = 0; k < 2 * KG; k += 4) {
           const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KSC + (8 * kb + 4 * hh) * KG / 2 + k);
-          sw[k] = s4.x; sw[k + 1] = s4.y; sw[k + 2] = s4.z; sw[k + 3] = s4.w;
+          sw[hh][k] = s4.x; sw[hh][k + 1] = s4.y; sw[hh][k + 2] = s4.z; sw[hh][k + 3] = s4.w;
           if constexpr (KAFF) {
             const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KBS + (8 * kb + 4 * hh) * KG / 2 + k);
-            bw[k] = b4.x; bw[k + 1] = b4.y; bw[k + 2] = b4.z; bw[k + 3] = b4.w;
+            bw[hh][k] = b4.x; bw[hh][k + 1] = b4.y; bw[hh][k + 2] = b4.z; bw[hh][k + 3] = b4.w;
           }
         }
-        float Lh[4] = {0.f, 0.f, 0.f, 0.f};
+      float Lh[2][4];
 #pragma unroll
-        for (int g = 0; g < KG; ++g) {
-          Frag ka;
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Lh[hh][i] = 0.f;
+      // D row 4 kb + i of tile hh is chunk token 8 kb + 4 hh + i: its
+      // (token, g) entry is half (i KG + g) % 2 of word (i KG + g) / 2; fp16
+      // scale / bias times an fp32 value: one v_fma_mix_f32 each
+      auto post = [&](const f32x4* d, int g) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = i * KG + g;
+            Lh[hh][i] = __builtin_fmaf(float(h2_of(sw[hh][e >> 1])[e & 1]), d[hh][i], Lh[hh][i]);
+            if constexpr (KAFF) Lh[hh][i] = __builtin_fmaf(float(h2_of(bw[hh][e >> 1])[e & 1]), qb[g], Lh[hh][i]);
+          }
+      };
+      f32x4 dprev[2];
+#pragma unroll
+      for (int g = 0; g < KG; ++g) {
+        Frag ka[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
           if constexpr (KBITS == 4) {
             const uint32_t w = Regs::kWordKeys ? R.kw[hh][g] : R.kr[hh][g].x;
             // nibble i of the word is channel i; channels i and i + 4 sit 16
@@ -539,10 +559,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
             // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
             // (nibbles 1, 3), and one packed add / fma makes it n - zp exactly
             const uint32_t w8 = w >> 8;
-            ka.u[0] = bits_of(h2_of((w & 0x000f000fu) | fp16_magic) + kadd0);
-            ka.u[1] = bits_of(h2_of((w & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
-            ka.u[2] = bits_of(h2_of((w8 & 0x000f000fu) | fp16_magic) + kadd0);
-            ka.u[3] = bits_of(h2_of((w8 & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+            ka[hh].u[0] = bits_of(h2_of((w & 0x000f000fu) | fp16_magic) + kadd0);
+            ka[hh].u[1] = bits_of(h2_of((w & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+            ka[hh].u[2] = bits_of(h2_of((w8 & 0x000f000fu) | fp16_magic) + kadd0);
+            ka[hh].u[3] = bits_of(h2_of((w8 & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
           } else {
             // byte i of the two words is channel i: one byte permute puts
             // bytes (2j, 2j + 1) under the magic's 0x64 bytes, giving the
@@ -550,27 +570,26 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
             // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
             const uint32_t wa = Regs::kWordKeys ? R.kw[hh][2 * g] : R.kr[hh][g].x;
             const uint32_t wb = Regs::kWordKeys ? R.kw[hh][2 * g + 1] : R.kr[hh][g].y;
-            ka.u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
-            ka.u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
-            ka.u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
-            ka.u[3] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05030502u)) + kadd0);
-          }
-          f32x4 d = {0.f, 0.f, 0.f, 0.f};
-          d = mfma(ka, qhi[g], d);
-          d = mfma(ka, qlo[g], d);
-          // D row 4 kb + i is chunk token 8 kb + 4 hh + i: its (token, g)
-          // entry is half (i KG + g) % 2 of word (i KG + g) / 2
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int e = i * KG + g;
-            // fp16 scale / bias times an fp32 value: one v_fma_mix_f32 each
-            Lh[i] = __builtin_fmaf(float(h2_of(sw[e >> 1])[e & 1]), d[i], Lh[i]);
-            if constexpr (KAFF) Lh[i] = __builtin_fmaf(float(h2_of(bw[e >> 1])[e & 1]), qb[g], Lh[i]);
+            ka[hh].u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
+            ka[hh].u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
+            ka[hh].u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
+            ka[hh].u[3] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05030502u)) + kadd0);
           }
         }
+        f32x4 d[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = Lh[i];
+        for (int hh = 0; hh < 2; ++hh) d[hh] = mfma(ka[hh], qhi[g], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) d[hh] = mfma(ka[hh], qlo[g], d[hh]);
+        if (g > 0) post(dprev, g - 1);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) dprev[hh] = d[hh];
       }
+      post(dprev, KG - 1);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = Lh[hh][i];
     }
   };
 
