@@ -311,3 +311,38 @@ def test_items_longer_than_one_metadata_batch(kfmt, vfmt, vgs, path):
         got = fused(list(qs), kp, vp, pages_per_split=pps).cpu().numpy()
         err = np.max(np.abs(got - want))
         assert err < KERNEL_TOL, f"path {path} pps {pps}: max-abs error {err}"
+
+
+@pytest.mark.parametrize("tpp", [128, 64])
+def test_fused_long_context_window_pools(tpp):
+    """The C5 pool shape on the MFMA kernel: head_dim 256, M0 affine 4-bit
+    keys and values with the newest pages exact (M3 fp16 keys and values in
+    the same pools), GQA 4, ragged sequences, split-K; run under path "mfma"
+    (the instance where two wavefronts share each work item)."""
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+    from dotcache_amd.decode import set_decode_path
+
+    set_decode_path("mfma")
+    rng = np.random.default_rng(256 + tpp)
+    hd, Q = 256, 4
+    lens = [tpp * 5 + 17, 1, tpp - 3, 3 * tpp, 2 * tpp + 1]
+    qs = (rng.normal(size=(len(lens), Q, hd)) / np.sqrt(hd)).astype(np.float32)
+    kpg, vpg = [], []
+    for n in lens:
+        pages_k, pages_v = [], []
+        k = rng.standard_t(4, size=(n, hd)).astype(np.float32)
+        v = rng.standard_t(4, size=(n, hd)).astype(np.float32)
+        n_pages = -(-n // tpp)
+        for i, s in enumerate(range(0, n, tpp)):
+            fmt = dict(mode="M3") if i >= n_pages - 1 and n_pages > 1 else dict(bits=4)  # the newest page exact
+            pages_k.append(O.encode_page(k[s:s + tpp], head_dim=hd, group_size=32, kind="K", token_start=s, **fmt))
+            pages_v.append(O.encode_page(v[s:s + tpp], head_dim=hd, group_size=32, kind="V", token_start=s, **fmt))
+        kpg.append(pages_k)
+        vpg.append(pages_v)
+    want = O.decode_grouped(qs, kpg, vpg)
+    kp = [[to_product_page(p) for p in g] for g in kpg]
+    vp = [[to_product_page(p) for p in g] for g in vpg]
+    for pps in (None, 1, 2):
+        got = fused(list(qs), kp, vp, pages_per_split=pps).cpu().numpy()
+        err = np.max(np.abs(got - want))
+        assert err < KERNEL_TOL, f"pps {pps}: max-abs error {err}"
