@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--decode-path", default="auto", choices=["auto", "generic", "mfma"],
                     help="auto: the MFMA kernel where the pages fit it; generic: the VALU kernel only; "
                          "mfma: the MFMA kernel only (an error where it does not fit)")
+    ap.add_argument("--head-block", type=int, default=0, choices=[0, 4, 8, 16],
+                    help="smallest head block of the MFMA kernel (0: automatic; 16: one key / value group "
+                         "per MFMA operand)")
     ap.add_argument("--key-bits", type=int, default=None,
                     help="re-code the configuration's M0 key pages at this width (a variant, not the "
                          "configuration's own line)")
@@ -63,7 +66,7 @@ def parse():
     return ap.parse_args()
 
 
-def profiled_traffic(workload: str, pages_per_split: int, decode_path: str):
+def profiled_traffic(workload: str, pages_per_split: int, decode_path: str, head_block: int):
     """HBM bytes per decode launch measured for this workload by the
     FETCH_SIZE / WRITE_SIZE runs summarised under profiles/ (calibrated
     against a copy of known size there), or None if none matches."""
@@ -72,8 +75,8 @@ def profiled_traffic(workload: str, pages_per_split: int, decode_path: str):
     for f in sorted((ROOT / "profiles").glob("*.md")):
         for m in re.finditer(r"<!-- traffic (\{.*?\}) -->", f.read_text()):
             rec = json.loads(m.group(1))
-            if (rec.get("workload"), rec.get("pages_per_split"), rec.get("decode_path")) == (
-                    workload, pages_per_split, decode_path):
+            if (rec.get("workload"), rec.get("pages_per_split"), rec.get("decode_path"), rec.get("head_block")) == (
+                    workload, pages_per_split, decode_path, head_block):
                 return float(rec["traffic_bytes"])
     return None
 
@@ -290,7 +293,7 @@ def main():
         encode_probe(max(args.steps, 1))
         return
 
-    from dotcache_amd.decode import set_decode_path
+    from dotcache_amd.decode import set_decode_path, set_mfma_head_block
     from dotcache_amd.workloads import SPECS, build_workload
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -298,6 +301,7 @@ def main():
     t0 = time.time()
     log(f"building workload {args.config} ...")
     set_decode_path(args.decode_path)
+    set_mfma_head_block(args.head_block)
     wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
                         scatter_pages=not args.contiguous_pages, key_bits=args.key_bits)
     spec = wl.spec
@@ -429,8 +433,8 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": profiled_traffic(spec.name, wl.plan.pages_per_split, args.decode_path),
-            "kernel": ("decode_mfma_kernel" if args.decode_path == "auto" else "decode_generic_kernel")
+            "traffic": profiled_traffic(spec.name, wl.plan.pages_per_split, args.decode_path, args.head_block),
+            "kernel": ("decode_generic_kernel" if args.decode_path == "generic" else "decode_mfma_kernel")
                       + " (dc_decode_paged, one launch per layer)",
             "launch_us": launch_ms * 1e3,
             "launch_us_stat": f"mean over {n_med} replays of one step's {L} decode launches (event per replay)",
@@ -440,6 +444,7 @@ def main():
             "bytes_per_launch": bytes_launch,
             "merge_us": merge_ms * 1e3,
             "decode_path": args.decode_path,
+            "head_block": args.head_block,
         },
         "cpu_baseline": cpu,
     }

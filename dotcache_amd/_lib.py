@@ -86,6 +86,7 @@ SIGNATURES = {
                                           C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
     "dc_decode_noalloc_scratch_bytes": (C.c_int64, []),
     "dc_set_decode_path": (C.c_int, [C.c_int32]),
+    "dc_set_mfma_head_block": (C.c_int, [C.c_int32]),
     "dc_lse_merge": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                C.c_void_p, C.c_void_p]),
 }

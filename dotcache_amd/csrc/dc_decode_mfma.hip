@@ -37,6 +37,21 @@
 //          VGS g + 8 (r / L) + r % L + L h with L = 128 / VGS, which lets
 //          every lane unpack its codes with one byte permute per pair of
 //          tokens.
+//
+// Group blocks.  With n_q <= 4 (or <= 8) most of the 16 columns / rows above
+// would be dead heads.  Instead they hold GB = 4 (or 2) copies of the NQB = 4
+// (8) heads, copy c = r / NQB working on group c of every block of GB
+// consecutive key / value groups:
+//   score  group g's query fragment is zero outside copy g % GB's columns, so
+//          the GB groups of a block accumulate into one tile pair, each
+//          copy's column holding its own group's dot product; one scale /
+//          bias step per block then serves GB groups, and rotate-adds within
+//          each 16-lane row sum the copies, which leaves every copy with the
+//          whole logit of its head.
+//   mix    row (c, q) is weight_q x the scale of group GB b + c: one weight x
+//          scale operand per block instead of one per group, and tile h of
+//          group g keeps only copy g % GB's rows.
+// The products are the same; only the lanes that form them change.
 #include <type_traits>
 
 #include "dc_common.h"
@@ -60,6 +75,13 @@ __device__ __forceinline__ f32x4 mfma(const Frag& a, const Frag& b, f32x4 c) {
 
 __device__ __forceinline__ uint32_t bits_of(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 h2_of(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// The value of lane (l - N) mod 16 of the lane's row of 16 (DPP row rotate).
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  static_assert(N > 0 && N < 16, "row rotate by 1 .. 15");
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + N, 0xf, 0xf, false));
+}
 
 // fp16 pair (lo, hi) from two floats, round to nearest even.
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) { return bits_of(h2{(_Float16)lo, (_Float16)hi}); }
@@ -106,8 +128,15 @@ struct MfmaCfg {
   static constexpr int KSW = 16 * KG;          // key scale words per chunk ([32][KG] fp16)
   static constexpr int NVS = (VSW + 63) / 64;
   static constexpr int NKS = (KSW + 63) / 64;
-  static constexpr int VPAY = 0, VSC = VG * GSTRIDE, VBS = VSC + VSW, KSC = VBS + VSW, KBS = KSC + KSW;
-  static constexpr int STAGE = KBS + KSW;  // words of one staged chunk
+  // scales / biases are staged as loaded ([32][G] fp16) or, where a lane
+  // needs one group of 8 consecutive tokens (group blocks), transposed:
+  // [G][SP] fp16, row pitch SP = 40 halves (16-byte aligned rows, and the
+  // transposing 16-bit stores of one instruction spread over the banks)
+  static constexpr int SP = 40;
+  static constexpr int VSR = VSW > VG * SP / 2 ? VSW : VG * SP / 2;  // words of one value scale region
+  static constexpr int KSR = KSW > KG * SP / 2 ? KSW : KG * SP / 2;
+  static constexpr int VPAY = 0, VSC = VG * GSTRIDE, VBS = VSC + VSR, KSC = VBS + VSR, KBS = KSC + KSR;
+  static constexpr int STAGE = KBS + KSR;  // words of one staged chunk
   static_assert(VG * 8 * W % 64 == 0, "value pieces must spread evenly over the wave");
   static_assert(W % 4 == 0, "value code rows are staged in 16-byte pieces");
 };
@@ -141,13 +170,22 @@ struct PageMeta {
 // KBITS: code width of the pool's M0 keys (4 or 8).  KAFF / VAFF: the key /
 // value pool may hold affine M0 pages (bias terms); false drops that code
 // entirely.
-template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF>
+//
+// NQB: query heads per block of the MFMA's 16 columns (score) / rows (mix),
+// 4, 8 or 16.  Below 16 the 16 slots hold GB = 16 / NQB copies of the NQB
+// heads, and copy c works on group c of each block of GB consecutive
+// groups (see "Group blocks" above).
+template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF, int NQB>
 __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   static_assert(KBITS == 4 || KBITS == 8, "M0 keys are 4- or 8-bit");
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
   using Regs = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS>;
   constexpr int KBLK = 4 * KBITS;  // bytes of one (token, group) key code block
   constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W, NACC = Cfg::NACC;
+  static_assert(NQB == 4 || NQB == 8 || NQB == 16, "4, 8 or 16 heads per block");
+  constexpr int GB = 16 / NQB;                // groups per block
+  constexpr int KNB = KG / GB, VNB = VG / GB;  // key / value group blocks
+  static_assert(KG % GB == 0 && VG % GB == 0, "key and value groups come in whole blocks");
   // two staged chunks in flight where the registers allow it
   constexpr bool kPipe = HD <= 128 && !(VM3 && KMODE == KEYS_MIXED);
   __shared__ uint32_t lds_all[(kPipe ? 2 : 1) * Cfg::STAGE];
@@ -180,7 +218,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   const int r = lane & 15, kb = lane >> 4;
   const int nq = a.n_q;
   const int CAP = a.kpool.geometry.page_capacity;
-  const bool head_live = r < nq;
+  // this lane's score column / mix row: head qh of group copy gsel
+  const int qh = r % NQB, gsel = r / NQB;
+  const bool head_live = qh < nq;
 
   // The prologue's loads go out in two rounds: the queries and the first
   // page batch's table entries together, then the descriptors those name.
@@ -188,7 +228,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // resource), so no load waits on a branch.
   // ---- queries, raw: lane (r, kb) holds channels 32 g + 8 kb + i of head r ----
   const int64_t qbase = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * nq * HD;
-  const int64_t qrow = qbase + int64_t(head_live ? r : 0) * HD + 8 * kb;
+  const int64_t qrow = qbase + int64_t(head_live ? qh : 0) * HD + 8 * kb;
   const bool q_f32 = a.queries_dtype == DC_F32;
   u32x4 qraw[2 * KG];  // fp32: two 16-byte pieces per group; fp16 / bf16: one
   if (q_f32) {
@@ -236,8 +276,11 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // converted once, after the item's first chunk loads are issued, so the
   // conversion overlaps them
   const float qmul = a.q_scale * kLog2e;
+  // B fragments of group g are zero in the columns of the other group
+  // copies (g % GB != gsel); qsum[b]: sum of head qh's channels of group
+  // GB b + gsel, the group this lane's column carries in block b
   Frag qhi[KG], qlo[KG];
-  float qsum[KG];
+  float qsum[KNB];
   bool q_ready = false;
   // (the per-chunk lambdas are always inlined: at head_dim 256 the compiler
   // otherwise calls some of them, passing the register sets through scratch)
@@ -279,14 +322,16 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         // where 4-bit M0 keys occur (the order their nibble unpack produces)
         const int c0 = kPairedQ ? i : 2 * i, c1 = kPairedQ ? i + 4 : 2 * i + 1;
         const float x0 = head_live ? qv[g][c0] * qmul : 0.f, x1 = head_live ? qv[g][c1] * qmul : 0.f;
-        qhi[g].u[i] = pack_h2(x0, x1);
-        const h2 hv = h2_of(qhi[g].u[i]);
-        qlo[g].u[i] = pack_h2(x0 - float(hv[0]), x1 - float(hv[1]));
+        const bool mine = GB == 1 || g % GB == gsel;
+        const uint32_t hi = pack_h2(x0, x1);
+        const h2 hv = h2_of(hi);
+        qhi[g].u[i] = mine ? hi : 0u;
+        qlo[g].u[i] = mine ? pack_h2(x0 - float(hv[0]), x1 - float(hv[1])) : 0u;
         s += x0 + x1;
       }
       s += __shfl_xor(s, 16, 64);
-      s += __shfl_xor(s, 32, 64);
-      qsum[g] = s;  // sum of group g of head r
+      s += __shfl_xor(s, 32, 64);  // sum of group g of head qh
+      if (g % GB == 0 || g % GB == gsel) qsum[g / GB] = s;  // ends as group GB b + gsel
     }
   };
 
@@ -314,9 +359,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   f32x4 acc[NACC];
 #pragma unroll
   for (int t = 0; t < NACC; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float bsum[VG];
+  float bsum[VNB];  // value bias sums of head qh, group GB b + gsel
 #pragma unroll
-  for (int g = 0; g < VG; ++g) bsum[g] = 0.f;
+  for (int b = 0; b < VNB; ++b) bsum[b] = 0.f;
   float m_ref = -INFINITY, l_part = 0.f;
   // the fp16 magic 0x6400 pair, held in a VGPR the compiler cannot see
   // through: (w & mask) | magic with a scalar mask is then one v_and_or_b32
@@ -440,12 +485,25 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       const int t = piece / (W / 4), wc = piece - t * (W / 4);
       *reinterpret_cast<u32x4*>(lds + Cfg::VPAY + g * Cfg::GSTRIDE + t * W + (t >> 3) * Cfg::PAD + 4 * wc) = R.vr[k];
     }
+    // word e of a [32][G] fp16 scale array holds (token e / (G / 2), groups
+    // 2 j, 2 j + 1), j = e % (G / 2); with group blocks its halves go to the
+    // transposed rows 2 j and 2 j + 1
+    auto put = [&](uint32_t* dst, uint32_t w, int e, int G) __attribute__((always_inline)) {
+      if constexpr (GB == 1) {
+        dst[e] = w;
+      } else {
+        const int t = e / (G / 2), j = e - t * (G / 2);
+        uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
+        d16[(2 * j) * Cfg::SP + t] = uint16_t(w);
+        d16[(2 * j + 1) * Cfg::SP + t] = uint16_t(w >> 16);
+      }
+    };
 #pragma unroll
     for (int k = 0; k < Cfg::NVS; ++k) {
       const int e = lane + 64 * k;
       if (Cfg::VSW % 64 == 0 || e < Cfg::VSW) {
-        lds[Cfg::VSC + e] = R.vs[k];
-        if constexpr (VAFF) lds[Cfg::VBS + e] = R.vb[k];
+        put(lds + Cfg::VSC, R.vs[k], e, VG);
+        if constexpr (VAFF) put(lds + Cfg::VBS, R.vb[k], e, VG);
       }
     }
     if constexpr (KMODE != KEYS_M3) {
@@ -453,8 +511,8 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       for (int k = 0; k < Cfg::NKS; ++k) {
         const int e = lane + 64 * k;
         if (Cfg::KSW % 64 == 0 || e < Cfg::KSW) {
-          lds[Cfg::KSC + e] = R.ks[k];
-          if constexpr (KAFF) lds[Cfg::KBS + e] = R.kbw[k];
+          put(lds + Cfg::KSC, R.ks[k], e, KG);
+          if constexpr (KAFF) put(lds + Cfg::KBS, R.kbw[k], e, KG);
         }
       }
     }
@@ -508,88 +566,134 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       const bool k_affine = KAFF && m.kfmt == DC_FMT_M0_AFFINE;
       const float zp = k_affine ? 0.f : float((1 << (KBITS - 1)) - 1);
       const float bf = k_affine ? 1.f : 0.f;
-      float qb[KG];  // bias weight of group g: sum of the query's group g (affine pages only)
+      float qb[KNB];  // bias weight of the column's group in block b: its query sum (affine pages only)
 #pragma unroll
-      for (int g = 0; g < KG; ++g) qb[g] = bf * qsum[g];
+      for (int b = 0; b < KNB; ++b) qb[b] = bf * qsum[b];
       // (1024 + n, 1024 + n') -> (n - zp, n' - zp); (1024 + 16 n, ..) / 16 - 64 - zp likewise
       const h2 kadd0 = {(_Float16)(-1024.f - zp), (_Float16)(-1024.f - zp)};
       const h2 kadd1 = {(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)};
       const h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-      // scales / biases of the D-row tokens 8 kb + 4 hh + i, all groups: [4][KG] fp16 per tile
-      uint32_t sw[2][2 * KG], bw[2][2 * KG];
+      // scales / biases of the D-row tokens 8 kb + 4 hh + i: with one group
+      // per block all groups, [4][KG] fp16 per tile, read up front; with
+      // group blocks the column's group GB b + gsel, read per block
+      uint32_t sw[2][GB == 1 ? 2 * KG : 1], bw[2][GB == 1 ? 2 * KG : 1];
+      if constexpr (GB == 1) {
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+        for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int k = 0; k < 2 * KG; k += 4) {
-          const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KSC + (8 * kb + 4 * hh) * KG / 2 + k);
-          sw[hh][k] = s4.x; sw[hh][k + 1] = s4.y; sw[hh][k + 2] = s4.z; sw[hh][k + 3] = s4.w;
+          for (int k = 0; k < 2 * KG; k += 4) {
+            const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KSC + (8 * kb + 4 * hh) * KG / 2 + k);
+            sw[hh][k] = s4.x; sw[hh][k + 1] = s4.y; sw[hh][k + 2] = s4.z; sw[hh][k + 3] = s4.w;
+            if constexpr (KAFF) {
+              const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KBS + (8 * kb + 4 * hh) * KG / 2 + k);
+              bw[hh][k] = b4.x; bw[hh][k + 1] = b4.y; bw[hh][k + 2] = b4.z; bw[hh][k + 3] = b4.w;
+            }
+          }
+      }
+      // group blocks: tokens 8 kb .. 8 kb + 7 of the column's group in block
+      // b, one 16-byte read of the transposed rows each
+      uint32_t sq[GB == 1 ? 1 : KNB][4], bq[GB == 1 ? 1 : KNB][4];
+      if constexpr (GB > 1) {
+#pragma unroll
+        for (int b = 0; b < KNB; ++b) {
+          const int o = ((GB * b + gsel) * Cfg::SP + 8 * kb) / 2;
+          const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KSC + o);
+          sq[b][0] = s4.x; sq[b][1] = s4.y; sq[b][2] = s4.z; sq[b][3] = s4.w;
           if constexpr (KAFF) {
-            const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KBS + (8 * kb + 4 * hh) * KG / 2 + k);
-            bw[hh][k] = b4.x; bw[hh][k + 1] = b4.y; bw[hh][k + 2] = b4.z; bw[hh][k + 3] = b4.w;
+            const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::KBS + o);
+            bq[b][0] = b4.x; bq[b][1] = b4.y; bq[b][2] = b4.z; bq[b][3] = b4.w;
           }
         }
+      }
       float Lh[2][4];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int i = 0; i < 4; ++i) Lh[hh][i] = 0.f;
-      // D row 4 kb + i of tile hh is chunk token 8 kb + 4 hh + i: its
-      // (token, g) entry is half (i KG + g) % 2 of word (i KG + g) / 2; fp16
-      // scale / bias times an fp32 value: one v_fma_mix_f32 each
-      auto post = [&](const f32x4* d, int g) __attribute__((always_inline)) {
+      // D row 4 kb + i of tile hh is chunk token 8 kb + 4 hh + i; fp16 scale /
+      // bias times an fp32 value: one v_fma_mix_f32 each
+      auto post = [&](const f32x4* d, int b) __attribute__((always_inline)) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int e = i * KG + g;
-            Lh[hh][i] = __builtin_fmaf(float(h2_of(sw[hh][e >> 1])[e & 1]), d[hh][i], Lh[hh][i]);
-            if constexpr (KAFF) Lh[hh][i] = __builtin_fmaf(float(h2_of(bw[hh][e >> 1])[e & 1]), qb[g], Lh[hh][i]);
+            float sc, bs;
+            if constexpr (GB == 1) {
+              const int e = i * KG + b;  // (token, g) entry: half e % 2 of word e / 2
+              sc = float(h2_of(sw[hh][e >> 1])[e & 1]);
+              bs = KAFF ? float(h2_of(bw[hh][e >> 1])[e & 1]) : 0.f;
+            } else {
+              const int t = 4 * hh + i;  // token 8 kb + t: half t % 2 of word t / 2
+              sc = float(h2_of(sq[b][t >> 1])[t & 1]);
+              bs = KAFF ? float(h2_of(bq[b][t >> 1])[t & 1]) : 0.f;
+            }
+            Lh[hh][i] = __builtin_fmaf(sc, d[hh][i], Lh[hh][i]);
+            if constexpr (KAFF) Lh[hh][i] = __builtin_fmaf(bs, qb[b], Lh[hh][i]);
           }
       };
+      // block b: the MFMAs of its GB groups accumulate into one tile pair
+      // (the other copies' query columns are zero), then block b - 1 is
+      // scaled while they run
       f32x4 dprev[2];
 #pragma unroll
-      for (int g = 0; g < KG; ++g) {
-        Frag ka[2];
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          if constexpr (KBITS == 4) {
-            const uint32_t w = Regs::kWordKeys ? R.kw[hh][g] : R.kr[hh][g].x;
-            // nibble i of the word is channel i; channels i and i + 4 sit 16
-            // bits apart, so one mask and the fp16 magic 0x6400 give the pair
-            // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
-            // (nibbles 1, 3), and one packed add / fma makes it n - zp exactly
-            const uint32_t w8 = w >> 8;
-            ka[hh].u[0] = bits_of(h2_of((w & 0x000f000fu) | fp16_magic) + kadd0);
-            ka[hh].u[1] = bits_of(h2_of((w & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
-            ka[hh].u[2] = bits_of(h2_of((w8 & 0x000f000fu) | fp16_magic) + kadd0);
-            ka[hh].u[3] = bits_of(h2_of((w8 & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
-          } else {
-            // byte i of the two words is channel i: one byte permute puts
-            // bytes (2j, 2j + 1) under the magic's 0x64 bytes, giving the
-            // pair (1024 + n_2j, 1024 + n_2j+1), and one packed add makes
-            // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
-            const uint32_t wa = Regs::kWordKeys ? R.kw[hh][2 * g] : R.kr[hh][g].x;
-            const uint32_t wb = Regs::kWordKeys ? R.kw[hh][2 * g + 1] : R.kr[hh][g].y;
-            ka[hh].u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
-            ka[hh].u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
-            ka[hh].u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
-            ka[hh].u[3] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05030502u)) + kadd0);
-          }
-        }
+      for (int b = 0; b < KNB; ++b) {
         f32x4 d[2];
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) d[hh] = mfma(ka[hh], qhi[g], f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int hh = 0; hh < 2; ++hh) d[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) d[hh] = mfma(ka[hh], qlo[g], d[hh]);
-        if (g > 0) post(dprev, g - 1);
+        for (int gi = 0; gi < GB; ++gi) {
+          const int g = GB * b + gi;
+          Frag ka[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            if constexpr (KBITS == 4) {
+              const uint32_t w = Regs::kWordKeys ? R.kw[hh][g] : R.kr[hh][g].x;
+              // nibble i of the word is channel i; channels i and i + 4 sit 16
+              // bits apart, so one mask and the fp16 magic 0x6400 give the pair
+              // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
+              // (nibbles 1, 3), and one packed add / fma makes it n - zp exactly
+              const uint32_t w8 = w >> 8;
+              ka[hh].u[0] = bits_of(h2_of((w & 0x000f000fu) | fp16_magic) + kadd0);
+              ka[hh].u[1] = bits_of(h2_of((w & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+              ka[hh].u[2] = bits_of(h2_of((w8 & 0x000f000fu) | fp16_magic) + kadd0);
+              ka[hh].u[3] = bits_of(h2_of((w8 & 0x00f000f0u) | fp16_magic) * k16 + kadd1);
+            } else {
+              // byte i of the two words is channel i: one byte permute puts
+              // bytes (2j, 2j + 1) under the magic's 0x64 bytes, giving the
+              // pair (1024 + n_2j, 1024 + n_2j+1), and one packed add makes
+              // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
+              const uint32_t wa = Regs::kWordKeys ? R.kw[hh][2 * g] : R.kr[hh][g].x;
+              const uint32_t wb = Regs::kWordKeys ? R.kw[hh][2 * g + 1] : R.kr[hh][g].y;
+              ka[hh].u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
+              ka[hh].u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
+              ka[hh].u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
+              ka[hh].u[3] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05030502u)) + kadd0);
+            }
+          }
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) d[hh] = mfma(ka[hh], qhi[g], d[hh]);
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) d[hh] = mfma(ka[hh], qlo[g], d[hh]);
+        }
+        if (b > 0) post(dprev, b - 1);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) dprev[hh] = d[hh];
       }
-      post(dprev, KG - 1);
+      post(dprev, KNB - 1);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = Lh[hh][i];
+    }
+    // group blocks: the column of copy c holds the part of the logit from
+    // the groups c carries; two (GB = 4) or one (GB = 2) rotate-adds within
+    // each row of 16 lanes give every copy the whole logit
+    if constexpr (GB > 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        Ls[e] += row_ror<NQB>(Ls[e]);
+        if constexpr (GB == 4) Ls[e] += row_ror<2 * NQB>(Ls[e]);
+      }
     }
   };
 
@@ -612,8 +716,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       m_ref = m_new;
       l_part *= alpha;
 #pragma unroll
-      for (int g = 0; g < VG; ++g) bsum[g] *= alpha;
-      // D row 4 kb + i of the accumulators is head 4 kb + i: its alpha lives in lane 4 kb + i
+      for (int b = 0; b < VNB; ++b) bsum[b] *= alpha;
+      // D row 4 kb + i of the accumulators is head (4 kb + i) % NQB, as is
+      // lane 4 kb + i: its alpha lives there
       float arow[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * kb + i, 64);
@@ -656,48 +761,86 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       // nibble of its byte; one packed fma maps either to c - zp exactly
       const h2 vadd = VBITS == 4 && (jj & 1) ? h2{(_Float16)(-64.f - zp), (_Float16)(-64.f - zp)}
                                               : h2{(_Float16)(-1024.f - zp), (_Float16)(-1024.f - zp)};
-      // scales (and biases) of tokens 8 kb + e, all groups: [8][VG] fp16 = 4 VG words
-      uint32_t sw[4 * VG], bw[4 * VG];
+      // scales (and biases) of tokens 8 kb + e: with one group per block all
+      // groups, [8][VG] fp16 = 4 VG words read up front; with group blocks
+      // the row's group GB b + gsel, read per block
+      uint32_t sw[GB == 1 ? 4 * VG : 1], bw[GB == 1 ? 4 * VG : 1];
+      if constexpr (GB == 1) {
 #pragma unroll
-      for (int k = 0; k < 4 * VG; k += 4) {
-        const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VSC + 4 * VG * kb + k);
-        sw[k] = s4.x; sw[k + 1] = s4.y; sw[k + 2] = s4.z; sw[k + 3] = s4.w;
-        if constexpr (VAFF) {
-          const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VBS + 4 * VG * kb + k);
-          bw[k] = b4.x; bw[k + 1] = b4.y; bw[k + 2] = b4.z; bw[k + 3] = b4.w;
+        for (int k = 0; k < 4 * VG; k += 4) {
+          const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VSC + 4 * VG * kb + k);
+          sw[k] = s4.x; sw[k + 1] = s4.y; sw[k + 2] = s4.z; sw[k + 3] = s4.w;
+          if constexpr (VAFF) {
+            const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VBS + 4 * VG * kb + k);
+            bw[k] = b4.x; bw[k + 1] = b4.y; bw[k + 2] = b4.z; bw[k + 3] = b4.w;
+          }
         }
       }
+      uint32_t sq[GB == 1 ? 1 : VNB][4], bq[GB == 1 ? 1 : VNB][4];
+      if constexpr (GB > 1) {
 #pragma unroll
-      for (int g = 0; g < VG; ++g) {
+        for (int b = 0; b < VNB; ++b) {
+          const int o = ((GB * b + gsel) * Cfg::SP + 8 * kb) / 2;
+          const u32x4 s4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VSC + o);
+          sq[b][0] = s4.x; sq[b][1] = s4.y; sq[b][2] = s4.z; sq[b][3] = s4.w;
+          if constexpr (VAFF) {
+            const u32x4 b4 = *reinterpret_cast<const u32x4*>(lds + Cfg::VBS + o);
+            bq[b][0] = b4.x; bq[b][1] = b4.y; bq[b][2] = b4.z; bq[b][3] = b4.w;
+          }
+        }
+      }
+      auto vscale = [&](int e, int b) __attribute__((always_inline)) -> float {  // token 8 kb + e
+        if constexpr (GB == 1) {
+          const int x = e * VG + b;
+          return float(h2_of(sw[x >> 1])[x & 1]);
+        } else {
+          return float(h2_of(sq[b][e >> 1])[e & 1]);
+        }
+      };
+      auto vbias = [&](int e, int b) __attribute__((always_inline)) -> float {
+        if constexpr (GB == 1) {
+          const int x = e * VG + b;
+          return float(h2_of(bw[x >> 1])[x & 1]);
+        } else {
+          return float(h2_of(bq[b][e >> 1])[e & 1]);
+        }
+      };
+      // block b: one weight x scale operand serves its GB groups (row copy c
+      // carries group GB b + c; the other copies' rows of a group's tiles
+      // are never stored)
+#pragma unroll
+      for (int b = 0; b < VNB; ++b) {
         Frag fa_hi, fa_res;
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const int e0 = (2 * pp) * VG + g, e1 = (2 * pp + 1) * VG + g;  // (token, group) entries
           // weight x fp16 scale straight to fp16 high and residual parts
-          const Split2 sp = split_products(pw[2 * pp], float(h2_of(sw[e0 >> 1])[e0 & 1]), pw[2 * pp + 1],
-                                           float(h2_of(sw[e1 >> 1])[e1 & 1]));
+          const Split2 sp = split_products(pw[2 * pp], vscale(2 * pp, b), pw[2 * pp + 1], vscale(2 * pp + 1, b));
           fa_hi.u[pp] = sp.hi;
           fa_res.u[pp] = sp.res;
           if constexpr (VAFF) {  // fp16 bias times weight: one v_fma_mix_f32 each
-            bsum[g] = __builtin_fmaf(float(h2_of(bw[e0 >> 1])[e0 & 1]), pb[2 * pp], bsum[g]);
-            bsum[g] = __builtin_fmaf(float(h2_of(bw[e1 >> 1])[e1 & 1]), pb[2 * pp + 1], bsum[g]);
+            bsum[b] = __builtin_fmaf(vbias(2 * pp, b), pb[2 * pp], bsum[b]);
+            bsum[b] = __builtin_fmaf(vbias(2 * pp + 1, b), pb[2 * pp + 1], bsum[b]);
           }
         }
-        const uint32_t* P = lds + Cfg::VPAY + g * Cfg::GSTRIDE + vrow;  // token 8 kb + e at P[e W]
 #pragma unroll
-        for (int h = 0; h < H; ++h) {
-          Frag fb;
+        for (int gi = 0; gi < GB; ++gi) {
+          const int g = GB * b + gi;
+          const uint32_t* P = lds + Cfg::VPAY + g * Cfg::GSTRIDE + vrow;  // token 8 kb + e at P[e W]
 #pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t x =
-                __builtin_amdgcn_perm(P[(2 * pp + 1) * W + vword[h]], P[(2 * pp) * W + vword[h]], vsel[h]);
-            if constexpr (VBITS == 4)
-              fb.u[pp] = bits_of(h2_of((x & nib_mask) | 0x64006400u) * nib_mul + vadd);
-            else
-              fb.u[pp] = bits_of(h2_of(x | 0x64006400u) + vadd);
+          for (int h = 0; h < H; ++h) {
+            Frag fb;
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+              const uint32_t x =
+                  __builtin_amdgcn_perm(P[(2 * pp + 1) * W + vword[h]], P[(2 * pp) * W + vword[h]], vsel[h]);
+              if constexpr (VBITS == 4)
+                fb.u[pp] = bits_of(h2_of((x & nib_mask) | 0x64006400u) * nib_mul + vadd);
+              else
+                fb.u[pp] = bits_of(h2_of(x | 0x64006400u) + vadd);
+            }
+            acc[g * H + h] = mfma(fa_hi, fb, acc[g * H + h]);
+            acc[g * H + h] = mfma(fa_res, fb, acc[g * H + h]);
           }
-          acc[g * H + h] = mfma(fa_hi, fb, acc[g * H + h]);
-          acc[g * H + h] = mfma(fa_res, fb, acc[g * H + h]);
         }
       }
     } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): gather columns from the rows
@@ -872,44 +1015,64 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   l += __shfl_xor(l, 32, 64);  // head r
   if constexpr (VAFF) {
 #pragma unroll
-    for (int g = 0; g < VG; ++g) {
-      bsum[g] += __shfl_xor(bsum[g], 16, 64);
-      bsum[g] += __shfl_xor(bsum[g], 32, 64);
+    for (int b = 0; b < VNB; ++b) {
+      bsum[b] += __shfl_xor(bsum[b], 16, 64);
+      bsum[b] += __shfl_xor(bsum[b], 32, 64);
     }
   }
   const bool final_out = it.partial < 0;
   if (!final_out && it.partial >= a.max_partials) return;
   float* dst = final_out ? a.out + qbase : a.part_o + int64_t(it.partial) * nq * HD;
-  // D row 4 kb + i is head q = 4 kb + i, whose sum and bias sums live in lane q
-  float inv[4], bq[4][VG];
+  // D row 4 kb + i is head q = (4 kb + i) % NQB of group copy c = 4 kb / NQB
+  // (every i: NQB is a multiple of 4); lane 4 kb + i holds the same head and
+  // copy, so q's sum and copy c's bias sums live there.  Rows of copy c are
+  // stored for the groups c carries (all groups when GB = 1).
+  const int orow = (4 * kb) % NQB, ocopy = (4 * kb) / NQB;
+  float inv[4], bq[4][VNB];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float lq = __shfl(l, 4 * kb + i, 64);
     inv[i] = final_out ? 1.f / fmaxf(lq, 1e-30f) : 1.f;
 #pragma unroll
-    for (int g = 0; g < VG; ++g) bq[i][g] = VAFF ? __shfl(bsum[g], 4 * kb + i, 64) : 0.f;
+    for (int b = 0; b < VNB; ++b) bq[i][b] = VAFF ? __shfl(bsum[b], 4 * kb + i, 64) : 0.f;
   }
-  // one per-lane pointer (row 4 kb, column dcol); every store is a constant offset from it
-  float* dq = dst + 4 * kb * HD + dcol;
+  // one per-lane pointer (head orow, column dcol); every store is a constant offset from it
+  float* dq = dst + orow * HD + dcol;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    if (4 * kb + i < nq)
+    if (orow + i < nq)
 #pragma unroll
       for (int g = 0; g < VG; ++g)
+        if (GB == 1 || g % GB == ocopy)
 #pragma unroll
-        for (int h = 0; h < H; ++h)
-          dq[i * HD + VGS * g + LPW4 * h] = (acc[g * H + h][i] * (1.f / kVS) + bq[i][g]) * inv[i];
-  if (!final_out && kb == 0 && head_live) {
+          for (int h = 0; h < H; ++h)
+            dq[i * HD + VGS * g + LPW4 * h] = (acc[g * H + h][i] * (1.f / kVS) + bq[i][g / GB]) * inv[i];
+  if (!final_out && kb == 0 && r < nq) {  // heads r < nq (copy 0)
     a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 0] = m_ref;
     a.part_ml[(int64_t(it.partial) * nq + r) * 2 + 1] = l;
   }
 }
 
-template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF>
+template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF, int NQB = 16>
 static int launch_t(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, KBITS, VBITS, VM3, KAFF, VAFF>), dim3(uint32_t(a.n_items)),
-                     dim3(64), 0, stream, a);
+  hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, KBITS, VBITS, VM3, KAFF, VAFF, NQB>),
+                     dim3(uint32_t(a.n_items)), dim3(64), 0, stream, a);
   return check_hip(hipGetLastError(), "decode_mfma_kernel launch");
+}
+
+// Smallest head block a launch may use (0 = automatic: 4, 8 or 16).
+static int g_min_nqb = 0;
+
+// The smallest head block that holds n_q, from QMIN (the smallest the
+// instance's group counts allow) up.
+template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF, int QMIN>
+static int launch_q(const DecodeArgs& a, hipStream_t stream) {
+  const int nq = a.n_q > g_min_nqb ? a.n_q : g_min_nqb;
+  if constexpr (QMIN <= 4)
+    if (nq <= 4) return launch_t<HD, VGS, KMODE, KBITS, VBITS, VM3, KAFF, VAFF, 4>(a, stream);
+  if constexpr (QMIN <= 8)
+    if (nq <= 8) return launch_t<HD, VGS, KMODE, KBITS, VBITS, VM3, KAFF, VAFF, 8>(a, stream);
+  return launch_t<HD, VGS, KMODE, KBITS, VBITS, VM3, KAFF, VAFF, 16>(a, stream);
 }
 
 static constexpr uint64_t fbit(int fmt, int bits) { return uint64_t(1) << (fmt * 9 + bits); }
@@ -937,26 +1100,27 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   const int hd = kg.head_dim, vgs = vg.group_size;
   int rc = -1;
   // specialised instantiations for the common pools (every BASELINE
-  // configuration, and 8-bit keys at head_dim 128), a general one per
-  // shape and code widths otherwise (KEYS_M3 ignores kbits)
-#define DC_EXACT(HD_, VGS_, KM_, KB_, VB_, VM3_, KA_, VA_)                                                 \
+  // configuration, and 8-bit keys at head_dim 128), each with head blocks
+  // from QM_ up, and a general one per shape and code widths otherwise
+  // (KEYS_M3 ignores kbits)
+#define DC_EXACT(HD_, VGS_, KM_, KB_, VB_, VM3_, KA_, VA_, QM_)                                            \
   if (rc < 0 && hd == HD_ && vgs == VGS_ && kmode == KM_ && (KM_ == KEYS_M3 || kbits == KB_) &&          \
       vbits == VB_ && vm3 == VM3_ && kaff == KA_ && vaff == VA_)                                         \
-    rc = launch_t<HD_, VGS_, KM_, KB_, VB_, VM3_, KA_, VA_>(a, stream);
+    rc = launch_q<HD_, VGS_, KM_, KB_, VB_, VM3_, KA_, VA_, QM_>(a, stream);
 #define DC_GENERAL(HD_, VGS_, VB_)                                                    \
   if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_)                             \
     rc = kbits == 8 ? launch_t<HD_, VGS_, KEYS_MIXED, 8, VB_, true, true, true>(a, stream) \
                     : launch_t<HD_, VGS_, KEYS_MIXED, 4, VB_, true, true, true>(a, stream);
-  DC_EXACT(64, 32, KEYS_M0, 4, 4, false, false, false)     // config 1
-  DC_EXACT(64, 32, KEYS_M0, 4, 4, false, true, true)       // config 2
-  DC_EXACT(128, 32, KEYS_M3, 4, 4, false, false, false)    // config 3
-  DC_EXACT(128, 64, KEYS_MIXED, 4, 8, false, true, false)  // config 4
-  DC_EXACT(128, 64, KEYS_M0, 4, 8, false, true, false)
-  DC_EXACT(128, 32, KEYS_M0, 4, 4, false, true, true)
-  DC_EXACT(256, 32, KEYS_MIXED, 4, 4, true, true, true)  // config 5 (fp16 recent window)
-  DC_EXACT(256, 32, KEYS_M0, 4, 4, false, true, true)
-  DC_EXACT(128, 32, KEYS_M0, 8, 4, false, true, true)  // 8-bit keys, 4-bit values
-  DC_EXACT(128, 32, KEYS_M0, 8, 8, false, true, true)  // 8-bit keys and values
+  DC_EXACT(64, 32, KEYS_M0, 4, 4, false, false, false, 8)     // config 1
+  DC_EXACT(64, 32, KEYS_M0, 4, 4, false, true, true, 8)       // config 2
+  DC_EXACT(128, 32, KEYS_M3, 4, 4, false, false, false, 16)   // config 3 (blocks of 8: slower)
+  DC_EXACT(128, 64, KEYS_MIXED, 4, 8, false, true, false, 8)  // config 4
+  DC_EXACT(128, 64, KEYS_M0, 4, 8, false, true, false, 8)
+  DC_EXACT(128, 32, KEYS_M0, 4, 4, false, true, true, 4)
+  DC_EXACT(256, 32, KEYS_MIXED, 4, 4, true, true, true, 4)  // config 5 (fp16 recent window)
+  DC_EXACT(256, 32, KEYS_M0, 4, 4, false, true, true, 4)
+  DC_EXACT(128, 32, KEYS_M0, 8, 4, false, true, true, 4)  // 8-bit keys, 4-bit values
+  DC_EXACT(128, 32, KEYS_M0, 8, 8, false, true, true, 4)  // 8-bit keys and values
   DC_GENERAL(64, 32, 4)
   DC_GENERAL(64, 32, 8)
   DC_GENERAL(64, 64, 4)
@@ -977,3 +1141,10 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
 }
 
 }  // namespace dc
+
+extern "C" int dc_set_mfma_head_block(int32_t nqb) {
+  if (nqb != 0 && nqb != 4 && nqb != 8 && nqb != 16)
+    return dc::fail(DC_EINVAL, "MFMA head block must be 0 (automatic), 4, 8 or 16");
+  dc::g_min_nqb = nqb;
+  return DC_OK;
+}

@@ -167,6 +167,17 @@ def set_decode_path(path: str) -> None:
     _lib.check(_lib.lib().dc_set_decode_path(_PATHS[path]), "dc_set_decode_path")
 
 
+def set_mfma_head_block(nqb: int) -> None:
+    """Smallest head block of the MFMA kernel: 0 (automatic), 4, 8 or 16.
+    With a block of 4 or 8 heads the kernel's 16 MFMA slots carry 4 or 2
+    copies of the heads, each on its own key / value group; 16 keeps one
+    group per MFMA operand (both layouts give the same results to fp32
+    rounding)."""
+    if nqb not in (0, 4, 8, 16):
+        raise ValueError("MFMA head block must be 0, 4, 8 or 16")
+    _lib.check(_lib.lib().dc_set_mfma_head_block(int(nqb)), "dc_set_mfma_head_block")
+
+
 def workspace_bytes(plan: DecodePlan, n_q: int, head_dim: int) -> int:
     return int(_lib.lib().dc_decode_workspace_bytes(plan.n_partials, n_q, head_dim))
 

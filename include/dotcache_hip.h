@@ -326,6 +326,16 @@ int64_t dc_decode_noalloc_scratch_bytes(void);
  * which kernel ran).  Host only; not thread-safe. */
 int dc_set_decode_path(int32_t path);
 
+/* Process-wide head block of the MFMA kernel: the 16 MFMA score columns and
+ * mix rows hold 16 / nqb copies of nqb query heads, each copy working on
+ * its own key / value group, so a launch with n_q <= 4 or <= 8 scales 4 or
+ * 2 groups per operand instead of one.  0 (default) picks the smallest
+ * block (4, 8 or 16) that holds n_q and that the pool's specialised kernel
+ * provides; 4, 8 or 16 sets the smallest block used (16: one group per
+ * MFMA operand, for cross-checking the layouts).  No counterpart in the
+ * reference (a kernel tuning switch).  Host only; not thread-safe. */
+int dc_set_mfma_head_block(int32_t nqb);
+
 #ifdef __cplusplus
 }
 #endif

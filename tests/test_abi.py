@@ -112,3 +112,21 @@ def test_decode_path_switch():
             set_decode_path("fast")
     finally:
         lib.dc_set_decode_path(0)
+
+
+def test_mfma_head_block_switch():
+    """Head blocks 0 (automatic), 4, 8 and 16 are accepted; anything else is
+    DC_EINVAL from the library and ValueError from the wrapper."""
+    from dotcache_amd.decode import set_mfma_head_block
+
+    lib = _lib.lib()
+    try:
+        for nqb in (0, 4, 8, 16):
+            assert lib.dc_set_mfma_head_block(nqb) == _lib.DC_OK
+            set_mfma_head_block(nqb)
+        for bad in (-1, 1, 2, 12, 32):
+            assert lib.dc_set_mfma_head_block(bad) == _lib.DC_EINVAL
+        with pytest.raises(ValueError):
+            set_mfma_head_block(2)
+    finally:
+        lib.dc_set_mfma_head_block(0)

@@ -15,12 +15,14 @@ def fresh_pools():
     """Every test prepares into fresh pools, so the formats one test puts in a
     pool never change which decode kernel another test gets."""
     from dotcache_amd.backends import clear_prepared_pools
-    from dotcache_amd.decode import set_decode_path
+    from dotcache_amd.decode import set_decode_path, set_mfma_head_block
 
     clear_prepared_pools()
     set_decode_path("auto")
+    set_mfma_head_block(0)
     yield
     set_decode_path("auto")
+    set_mfma_head_block(0)
     clear_prepared_pools()
 
 
@@ -177,6 +179,9 @@ FAST_CASES = [
     # 8-bit keys: specialised instances at head_dim 128, group 32 values
     (dict(bits=8), dict(bits=4), 128, 32, 6, 64),
     (dict(bits=8), dict(bits=8), 128, 32, 8, 64),
+    # head blocks of 4 with a dead head in every copy
+    (dict(bits=4), dict(bits=4), 128, 32, 3, 64),
+    (dict(bits=8), dict(bits=4), 128, 32, 2, 64),
     # and the general instances (symmetric keys, other shapes)
     (dict(bits=8, scheme="symmetric"), dict(bits=8, scheme="symmetric"), 128, 32, 4, 64),
     (dict(bits=8), dict(bits=8, scheme="symmetric"), 128, 64, 6, 64),
@@ -192,17 +197,20 @@ FAST_CASES = [
 KERNEL_TOL = 3e-4
 
 
-@pytest.mark.parametrize("path", ["mfma", "generic"])
+@pytest.mark.parametrize("path", ["mfma", "mfma16", "generic"])
 @pytest.mark.parametrize("kfmt,vfmt,hd,vgs,Q,tpp", FAST_CASES)
 def test_fused_kernels_match_oracle(kfmt, vfmt, hd, vgs, Q, tpp, path):
     """The MFMA kernel and the generic kernel on the same pages, with ragged
     groups, partial last pages, outlier channels and split-K.  Path "mfma"
     raises if the MFMA kernel does not take the call, so every case here is
-    shown to run on it."""
+    shown to run on it; "mfma16" is the MFMA kernel with one key / value
+    group per MFMA operand (head block 16) where "mfma" may use blocks of 4
+    or 8 heads."""
     from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
-    from dotcache_amd.decode import set_decode_path
+    from dotcache_amd.decode import set_decode_path, set_mfma_head_block
 
-    set_decode_path(path)
+    set_decode_path("mfma" if path == "mfma16" else path)
+    set_mfma_head_block(16 if path == "mfma16" else 0)
     rng = np.random.default_rng(hd * 7 + Q + tpp)
     lens = [tpp * 5 + 17, 1, tpp - 3, 3 * tpp]
     G = len(lens)
