@@ -141,21 +141,39 @@ struct MfmaCfg {
   static_assert(W % 4 == 0, "value code rows are staged in 16-byte pieces");
 };
 
-// Registers one chunk needs from HBM.  Every chunk issues the same loads
-// whatever its page formats, so the compiler never has to drain the queue to
-// merge register versions.
-template <int HD, int VGS, int VBITS, int KMODE, int KBITS>
+// Two staged chunks in flight where the registers allow it.
+template <int HD, int KMODE, bool VM3>
+constexpr bool pipelined() {
+  return HD <= 128 && !(VM3 && KMODE == KEYS_MIXED);
+}
+
+// Registers one chunk needs from HBM.  Keys: with ROWS (pools of mixed key
+// formats with chunks in flight) 16 bytes per (tile, group), an M3 row piece
+// or the 16-byte aligned piece of the M0 code block that holds this lane's
+// words; otherwise this lane's KW words of each M0 code block, and M3 rows
+// go straight to LDS.
+template <int HD, int VGS, int VBITS, int KMODE, int KBITS, bool ROWS>
 struct ChunkRegs {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  static constexpr bool kWordKeys = KMODE == KEYS_M0;
+  static constexpr bool kKeyWords = KMODE != KEYS_M3 && !ROWS;
   static constexpr int KW = KBITS / 4;  // code words of one lane's 8 channels
-  // keys: M3 row pieces (8 fp16) or 16 bytes from this lane's codes of the
-  // (token, group) block; a pool of M0 keys only needs this lane's KW words
-  u32x4 kr[kWordKeys ? 1 : 2][kWordKeys ? 1 : Cfg::KG];
-  uint32_t kw[kWordKeys ? 2 : 1][kWordKeys ? Cfg::KG * KW : 1];
+  u32x4 kr[ROWS ? 2 : 1][ROWS ? Cfg::KG : 1];
+  uint32_t kw[kKeyWords ? 2 : 1][kKeyWords ? Cfg::KG * KW : 1];
   u32x4 vr[Cfg::NVP];  // value code pieces, blob byte order
   uint32_t ks[Cfg::NKS], kbw[Cfg::NKS], vs[Cfg::NVS], vb[Cfg::NVS];  // scale / bias words
 };
+
+// Slot swizzle of the key rows staged in LDS: row t of PPR 16-byte pieces
+// keeps piece p at slot p ^ key_swz(t).  Bits {0, 1, 3, 4} of t (PPR >= 16)
+// or {1, 3, 4} (PPR = 8): the 16 rows one score read touches, 8 (r / 4) +
+// 4 hh + r % 4 for r < 16, get 16 (8) distinct values, which puts their
+// pieces in distinct 16-byte bank groups.  A bit selection, so it splits
+// over rows whose set bits are disjoint: key_swz(a | b) = key_swz(a) ^
+// key_swz(b).
+template <int PPR>
+__device__ __forceinline__ constexpr uint32_t key_swz(uint32_t t) {
+  return PPR >= 16 ? (t & 3u) | (((t >> 3) & 3u) << 2) : ((t >> 1) & 1u) | (((t >> 3) & 3u) << 1);
+}
 
 // One chunk: the page it belongs to (wave-uniform, in SGPRs) and its first token.
 struct PageMeta {
@@ -179,7 +197,10 @@ template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF,
 __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   static_assert(KBITS == 4 || KBITS == 8, "M0 keys are 4- or 8-bit");
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  using Regs = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS>;
+  constexpr bool kPipe = pipelined<HD, KMODE, VM3>();
+  // mixed key formats with chunks in flight: key rows / code pieces in registers
+  constexpr bool kRowRegs = KMODE == KEYS_MIXED && kPipe;
+  using Regs = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS, kRowRegs>;
   constexpr int KBLK = 4 * KBITS;  // bytes of one (token, group) key code block
   constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W, NACC = Cfg::NACC;
   static_assert(NQB == 4 || NQB == 8 || NQB == 16, "4, 8 or 16 heads per block");
@@ -187,20 +208,17 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   constexpr int KNB = KG / GB, VNB = VG / GB;  // key / value group blocks
   static_assert(KG % GB == 0 && VG % GB == 0, "key and value groups come in whole blocks");
   // two staged chunks in flight where the registers allow it
-  constexpr bool kPipe = HD <= 128 && !(VM3 && KMODE == KEYS_MIXED);
   __shared__ uint32_t lds_all[(kPipe ? 2 : 1) * Cfg::STAGE];
-  // M3-only keys at head_dim 128: each chunk's 32 key rows go straight from
-  // HBM into an LDS buffer (buffer_load ... lds), 1 KiB-contiguous per
-  // instruction, and the score reads them back in the MFMA's A layout.  Two
-  // buffers as separate objects, so a read of one waits only for its own
-  // loads.  Row t holds its 16-byte piece p at slot p ^ swz(t), swz(t) =
-  // bits {0, 1, 3, 4} of t, which puts the 16 rows one read touches in 16
-  // distinct bank groups.
-  constexpr bool kDmaK = kPipe && KMODE == KEYS_M3 && HD == 128;
+  // M3 keys (pools that may hold them): each chunk's 32 key rows go straight
+  // from HBM into an LDS buffer (buffer_load ... lds), 1 KiB-contiguous per
+  // instruction, and the score reads them back in the MFMA's A layout, with
+  // the slot swizzle key_swz.  One buffer per chunk in flight, as separate
+  // objects, so a read of one waits only for its own loads.
+  constexpr bool kDmaK = KMODE != KEYS_M0 && !kRowRegs;
   // pools with 4-bit M0 keys order each lane's 8 channels as pairs (i, i + 4)
   constexpr bool kPairedQ = KMODE != KEYS_M3 && KBITS == 4;
   __shared__ __attribute__((aligned(16))) uint32_t kbuf0[kDmaK ? 32 * HD / 2 : 1];
-  __shared__ __attribute__((aligned(16))) uint32_t kbuf1[kDmaK ? 32 * HD / 2 : 1];
+  __shared__ __attribute__((aligned(16))) uint32_t kbuf1[kDmaK && kPipe ? 32 * HD / 2 : 1];
   // key buffer 0 or 1, chosen at compile time (std::integral_constant), so
   // every LDS address the loads and reads use is a constant of one object
   auto kbuf = [&](auto bi) -> uint32_t* {
@@ -381,33 +399,48 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // blob's bytes, so an access past the page reads zeros instead of another
   // page): a per-lane offset fixed for the whole item, a wave-uniform chunk
   // offset and a constant, with no per-chunk address arithmetic in VGPRs.
-  uint32_t koff_m3[2], koff_m0[2];  // A-row token of tile hh: 8 (r / 4) + 4 hh + r % 4
+  // this lane's KW words (channels 8 kb .. 8 kb + 7) of the (token, group 0)
+  // code block of A-row token 8 (r / 4) + 4 hh + r % 4 in tile hh
+  uint32_t koff_m0[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) koff_m0[hh] = (8 * (r >> 2) + 4 * hh + (r & 3)) * KBLK + KBITS * kb;
+  // key registers by rows: the M3 row piece (channels 8 kb .. 8 kb + 7 of
+  // group 0), or 16 bytes of M0 codes that start at the lane's words; the
+  // chunk's last row (token 31: tile 1, r = 15) ends them at the lane's words
+  // instead, so no load reaches into the next chunk
+  const bool last_row = r == 15;
+  uint32_t koff_m3[2], koff_a[2];
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
     const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
-    koff_m3[hh] = (ta * HD + 8 * kb) * 2;                     // M3 row piece, channels 8 kb .. of group 0
-    // this lane's KW words (channels 8 kb .. 8 kb + 7) of the (token, group
-    // 0) code block; a 16-byte load from there (pools with M3 keys too) has
-    // them first and reads on inside the blob
-    koff_m0[hh] = ta * KBLK + KBITS * kb;
+    koff_m3[hh] = (ta * HD + 8 * kb) * 2;
+    koff_a[hh] = ta * KBLK + KBITS * kb - (hh == 1 && last_row ? 16u - KBITS : 0u);
   }
-  // key DMA: instruction i writes rows 4 i .. 4 i + 3 of the chunk; lane l
-  // takes row 4 i + l / 16, slot l % 16, i.e. source piece (l % 16) ^
-  // swz(row) with swz(row) = l / 16 + 4 ((i / 2) % 4): one offset per pair
-  uint32_t kdma[4];
+  // key DMA: rows of PPR pieces, RPI rows per instruction, NDMA instructions
+  // per chunk; instruction i writes rows RPI i .. RPI i + RPI - 1, lane l slot
+  // l % PPR of row RPI i + l / PPR, from source piece (l % PPR) ^ key_swz(row).
+  // The row's bits split into RPI i and l / PPR, so the lane's offset is
+  // kdma0 ^ 16 key_swz(RPI i): one register per distinct swizzle constant.
+  constexpr int PPR = HD / 8, RPI = 64 / PPR, NDMA = 32 / RPI;
+  const uint32_t kdma0 = uint32_t(lane / PPR) * PPR * 16 + 16u * (uint32_t(lane % PPR) ^ key_swz<PPR>(lane / PPR));
+  // (equal swizzle constants give equal values, which share a register; a
+  // literal bound: hipcc's host pass drops the kernel stubs when this array's
+  // size is a dependent constant)
+  static_assert(NDMA <= 16, "at most 16 DMA instructions per chunk");
+  uint32_t kdma[16];
 #pragma unroll
-  for (int ip = 0; ip < 4; ++ip) {
-    const uint32_t rw = uint32_t(lane >> 4), sw = rw | uint32_t(ip << 2);
-    kdma[ip] = rw * (HD * 2) + 16u * ((uint32_t(lane) & 15u) ^ sw);
-  }
-  // score read of tile hh, group g: row ta = 8 (r / 4) + 4 hh + r % 4 (swz(ta) = r), piece 4 g + kb
-  uint32_t krd[2][KG];
+  for (int i = 0; i < NDMA; ++i) kdma[i] = kdma0 ^ (16u * key_swz<PPR>(uint32_t(RPI * i)));
+  // score read of tile hh, group g: row ta = 8 (r / 4) + 4 hh + r % 4, piece
+  // 4 g + kb at slot (4 g + kb) ^ key_swz(ta); key_swz(ta) < 16, so group g
+  // reads krd[hh][g % 4] + 64 (g / 4) words
+  constexpr int KJ = KG < 4 ? KG : 4;
+  uint32_t krd[2][KJ];
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-    for (int g = 0; g < KG; ++g) {
+    for (int j = 0; j < KJ; ++j) {
       const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
-      krd[hh][g] = ta * (HD / 2) + 4u * ((uint32_t(4 * g + kb)) ^ uint32_t(r));  // in words
+      krd[hh][j] = ta * (HD / 2) + 4u * (uint32_t(4 * j + kb) ^ key_swz<PPR>(ta));  // in words
     }
   uint32_t voff[Cfg::NVP];
 #pragma unroll
@@ -420,42 +453,52 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
   auto load_chunk = [&](const PageMeta& m, Regs& R, auto kbi) __attribute__((always_inline)) {
     const int c0 = m.c0;
-    if constexpr (kDmaK) {
+    auto dma_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(m.krs, (__attribute__((address_space(3))) void*)(kbuf(kbi) + 256 * i),
-                                                 16, kdma[i >> 1], c0 * HD * 2 + 1024 * i, 0, kNT);
-    } else if constexpr (Regs::kWordKeys) {
+      for (int i = 0; i < NDMA; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(kbuf(kbi) + 256 * i),
+                                                 16, kdma[i], c0 * HD * 2 + 1024 * i, 0, kNT);
+    };
+    auto word_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const int co = c0 * KBLK + g * CAP * KBLK;
           if constexpr (KBITS == 4) {
-            R.kw[hh][g] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(koff_m0[hh]), co, kNT);
+            R.kw[hh][g] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(koff_m0[hh]), co, kNT);
           } else {
             typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-            const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(m.krs, int(koff_m0[hh]), co, kNT);
+            const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, int(koff_m0[hh]), co, kNT);
             R.kw[hh][2 * g] = x.x;
             R.kw[hh][2 * g + 1] = x.y;
           }
         }
-    } else {
+      // the scale / bias offsets are wave-uniform; readfirstlane says so, or
+      // the compiler wraps each of these loads in a per-value loop
+      const int ksc = __builtin_amdgcn_readfirstlane(int(m.ksc)), kbs = __builtin_amdgcn_readfirstlane(int(m.kbs));
+#pragma unroll
+      for (int k = 0; k < Cfg::NKS; ++k) {
+        R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(ksoff), ksc + c0 * KG * 2 + 256 * k, kNT);
+        if constexpr (KAFF)
+          R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(ksoff), kbs + c0 * KG * 2 + 256 * k, kNT);
+      }
+    };
+    if constexpr (kRowRegs) {
+      // both formats through the same loads (wave-uniform offsets), so every
+      // chunk issues the same loads and the compiler's counts of loads in
+      // flight stay exact across chunks of either format
       const bool km3 = key_is_m3(m);
       const int cbase = c0 * (km3 ? HD * 2 : KBLK);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const uint32_t lo = km3 ? koff_m3[hh] : koff_m0[hh];
+        const uint32_t lo = km3 ? koff_m3[hh] : koff_a[hh];
 #pragma unroll
         for (int g = 0; g < KG; ++g) {
           const int goff = km3 ? 64 * g : g * CAP * KBLK;
           R.kr[hh][g] = __builtin_amdgcn_raw_buffer_load_b128(m.krs, int(lo), cbase + goff, kNT);
         }
       }
-    }
-    // the scale / bias offsets are wave-uniform; readfirstlane says so, or
-    // the compiler wraps each of these loads in a per-value loop
-    if constexpr (KMODE != KEYS_M3) {
       const int ksc = __builtin_amdgcn_readfirstlane(int(m.ksc)), kbs = __builtin_amdgcn_readfirstlane(int(m.kbs));
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
@@ -463,6 +506,14 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         if constexpr (KAFF)
           R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), kbs + c0 * KG * 2 + 256 * k, kNT);
       }
+    } else if constexpr (KMODE == KEYS_M3) {
+      dma_keys(m.krs);
+    } else if constexpr (KMODE == KEYS_M0) {
+      word_keys(m.krs);
+    } else if (key_is_m3(m)) {  // one chunk in flight: a wave-uniform branch
+      dma_keys(m.krs);
+    } else {
+      word_keys(m.krs);
     }
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k)
@@ -526,7 +577,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     // tile hh x high / residual query part), the M0 path scales group g - 1
     // while the MFMAs of group g run
     if (key_is_m3(m)) {
-      if constexpr (kDmaK || !Regs::kWordKeys) {
+      if constexpr (kDmaK || kRowRegs) {
         f32x4 dh[2], dl[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) dh[hh] = dl[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -535,19 +586,19 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           Frag ka[2];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
-            if constexpr (kDmaK) {
-              const u32x4 x = *reinterpret_cast<const u32x4*>(kl + krd[hh][g]);
-              ka[hh].u[0] = x.x; ka[hh].u[1] = x.y; ka[hh].u[2] = x.z; ka[hh].u[3] = x.w;
+            // channels (0, 1), (2, 3), (4, 5), (6, 7) of the lane's 8
+            u32x4 x;
+            if constexpr (kRowRegs)
+              x = R.kr[hh][g];
+            else
+              x = *reinterpret_cast<const u32x4*>(kl + krd[hh][g % 4] + 64 * (g / 4));
+            if constexpr (kPairedQ) {  // -> (0, 4), (1, 5), (2, 6), (3, 7)
+              ka[hh].u[0] = __builtin_amdgcn_perm(x.z, x.x, 0x05040100u);
+              ka[hh].u[1] = __builtin_amdgcn_perm(x.z, x.x, 0x07060302u);
+              ka[hh].u[2] = __builtin_amdgcn_perm(x.w, x.y, 0x05040100u);
+              ka[hh].u[3] = __builtin_amdgcn_perm(x.w, x.y, 0x07060302u);
             } else {
-              const u32x4 x = R.kr[hh][g];  // channels (0, 1), (2, 3), (4, 5), (6, 7)
-              if constexpr (kPairedQ) {        // -> (0, 4), (1, 5), (2, 6), (3, 7)
-                ka[hh].u[0] = __builtin_amdgcn_perm(x.z, x.x, 0x05040100u);
-                ka[hh].u[1] = __builtin_amdgcn_perm(x.z, x.x, 0x07060302u);
-                ka[hh].u[2] = __builtin_amdgcn_perm(x.w, x.y, 0x05040100u);
-                ka[hh].u[3] = __builtin_amdgcn_perm(x.w, x.y, 0x07060302u);
-              } else {
-                ka[hh].u[0] = x.x; ka[hh].u[1] = x.y; ka[hh].u[2] = x.z; ka[hh].u[3] = x.w;
-              }
+              ka[hh].u[0] = x.x; ka[hh].u[1] = x.y; ka[hh].u[2] = x.z; ka[hh].u[3] = x.w;
             }
           }
 #pragma unroll
@@ -647,7 +698,13 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             if constexpr (KBITS == 4) {
-              const uint32_t w = Regs::kWordKeys ? R.kw[hh][g] : R.kr[hh][g].x;
+              uint32_t w;
+              if constexpr (kRowRegs) {
+                const u32x4 x = R.kr[hh][g];
+                w = hh == 1 && last_row ? x.w : x.x;
+              } else {
+                w = R.kw[hh][g];
+              }
               // nibble i of the word is channel i; channels i and i + 4 sit 16
               // bits apart, so one mask and the fp16 magic 0x6400 give the pair
               // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
@@ -662,8 +719,15 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
               // bytes (2j, 2j + 1) under the magic's 0x64 bytes, giving the
               // pair (1024 + n_2j, 1024 + n_2j+1), and one packed add makes
               // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
-              const uint32_t wa = Regs::kWordKeys ? R.kw[hh][2 * g] : R.kr[hh][g].x;
-              const uint32_t wb = Regs::kWordKeys ? R.kw[hh][2 * g + 1] : R.kr[hh][g].y;
+              uint32_t wa, wb;
+              if constexpr (kRowRegs) {
+                const u32x4 x = R.kr[hh][g];
+                wa = hh == 1 && last_row ? x.z : x.x;
+                wb = hh == 1 && last_row ? x.w : x.y;
+              } else {
+                wa = R.kw[hh][2 * g];
+                wb = R.kw[hh][2 * g + 1];
+              }
               ka[hh].u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
               ka[hh].u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
               ka[hh].u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
