@@ -144,7 +144,7 @@ struct MfmaCfg {
 // Two staged chunks in flight where the registers allow it.
 template <int HD, int KMODE, bool VM3>
 constexpr bool pipelined() {
-  return HD <= 128 && !(VM3 && KMODE == KEYS_MIXED);
+  return HD <= 128 && !VM3;
 }
 
 // Registers one chunk needs from HBM.  Keys: with ROWS (pools of mixed key
@@ -219,6 +219,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   constexpr bool kPairedQ = KMODE != KEYS_M3 && KBITS == 4;
   __shared__ __attribute__((aligned(16))) uint32_t kbuf0[kDmaK ? 32 * HD / 2 : 1];
   __shared__ __attribute__((aligned(16))) uint32_t kbuf1[kDmaK && kPipe ? 32 * HD / 2 : 1];
+  // M3 value rows of the chunk being mixed, by DMA in the same slot layout
+  // (pools that may hold M3 values; these are never pipelined)
+  static_assert(!(VM3 && kPipe), "pools with M3 values run one chunk in flight");
+  __shared__ __attribute__((aligned(16))) uint32_t vbuf[VM3 ? 32 * HD / 2 : 1];
   // key buffer 0 or 1, chosen at compile time (std::integral_constant), so
   // every LDS address the loads and reads use is a constant of one object
   auto kbuf = [&](auto bi) -> uint32_t* {
@@ -907,12 +911,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           }
         }
       }
-    } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): gather columns from the rows
-      // 16-bit buffer loads against a resource covering the page's valid
-      // rows only: a row at or past the token count reads zero, with no branch
-      const __amdgpu_buffer_rsrc_t vrows =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0, m.T * HD * 2, 0x00020000);
-      const uint32_t vbase = uint32_t(((m.c0 + 8 * kb) * HD + dcol) * 2);  // token 8 kb, column dcol of the chunk
+    } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): rows staged in vbuf
       Frag fa_hi, fa_res;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
@@ -920,22 +919,41 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         fa_hi.u[pp] = sp.hi;
         fa_res.u[pp] = sp.res;
       }
+      // B fragment of tile h of group g: column d = VGS g + dcol + LPW4 h of
+      // chunk tokens 8 kb + e; row t keeps piece d / 8 at slot (d / 8) ^
+      // key_swz(t).  A token at or past the page's count reads 0 (its
+      // weight is 0, and the row's bytes need not be finite).
+      const uint16_t* V = reinterpret_cast<const uint16_t*>(vbuf);
+      const int tvalid = m.T - m.c0 - 8 * kb;  // tokens 8 kb + e with e < tvalid are valid
 #pragma unroll
       for (int g = 0; g < VG; ++g)
 #pragma unroll
         for (int h = 0; h < H; ++h) {
-          const int dofs = (VGS * g + LPW4 * h) * 2;
+          const uint32_t d = uint32_t(VGS * g + dcol + LPW4 * h);
           Frag fb;
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(vrows, int(vbase), (2 * pp) * HD * 2 + dofs, 0);
-            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(vrows, int(vbase), (2 * pp + 1) * HD * 2 + dofs, 0);
+            const uint32_t t0 = uint32_t(8 * kb + 2 * pp), t1 = t0 + 1;
+            uint32_t lo = V[t0 * HD + 8 * ((d >> 3) ^ key_swz<PPR>(t0)) + (d & 7)];
+            uint32_t hi = V[t1 * HD + 8 * ((d >> 3) ^ key_swz<PPR>(t1)) + (d & 7)];
+            if (2 * pp >= tvalid) lo = 0;
+            if (2 * pp + 1 >= tvalid) hi = 0;
             fb.u[pp] = lo | (hi << 16);
           }
           acc[g * H + h] = mfma(fa_hi, fb, acc[g * H + h]);
           acc[g * H + h] = mfma(fa_res, fb, acc[g * H + h]);
         }
     }
+  };
+  // the M3 value rows of a chunk into vbuf, against a resource that ends at
+  // the page's last valid row
+  auto load_value_rows = [&](const PageMeta& m) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rows =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0, m.T * HD * 2, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rows, (__attribute__((address_space(3))) void*)(vbuf + 256 * i), 16,
+                                               kdma[i], m.c0 * HD * 2 + 1024 * i, 0, kNT);
   };
 
   // head_dim 256 converts up front: holding its raw queries across the first
@@ -1056,9 +1074,12 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       while (step(RB, RA, buf0, buf1, KB0{}, KB1{}) && step(RA, RB, buf1, buf0, KB1{}, KB0{})) {
       }
     } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
+      // (M3 value rows go to vbuf once the previous chunk's mix has read it)
       Regs R;
       PageMeta cur = chunk_meta(0);
       load_chunk(cur, R, KB0{});
+      if constexpr (VM3)
+        if (!is_m0(cur.vfmt)) load_value_rows(cur);
       prep_queries();
       for (int j = 0; j < total; ++j) {
         const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
@@ -1068,6 +1089,8 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         load_chunk(nm, R, KB0{});
         softmax_chunk(cur, Ls, pa);
         mix_chunk(cur, lds_all, pa);
+        if constexpr (VM3)
+          if (j + 1 < total && !is_m0(nm.vfmt)) load_value_rows(nm);
         cur = nm;
       }
     }
