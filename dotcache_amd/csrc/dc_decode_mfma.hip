@@ -200,7 +200,15 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   constexpr bool kPipe = pipelined<HD, KMODE, VM3>();
   // mixed key formats with chunks in flight: key rows / code pieces in registers
   constexpr bool kRowRegs = KMODE == KEYS_MIXED && kPipe;
-  using Regs = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS, kRowRegs>;
+  // Chunk-loop specialisations: FM_ANY takes every format the pool allows,
+  // checked per chunk; FM_M0 serves a batch of pages whose keys and values
+  // are all M0 (nearly every batch of a mixed pool), with the M3 paths and
+  // their registers compiled out.  Pipelined mixed pools get both (C4-like
+  // pools: 49.7 against 51.4 us); one chunk in flight (head_dim 256 with an
+  // fp16 window) measured no faster with both.
+  using FM_ANY = std::integral_constant<bool, false>;
+  using FM_M0 = std::integral_constant<bool, true>;
+  constexpr bool kTwoLoops = KMODE == KEYS_MIXED && kPipe;
   constexpr int KBLK = 4 * KBITS;  // bytes of one (token, group) key code block
   constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W, NACC = Cfg::NACC;
   static_assert(NQB == 4 || NQB == 8 || NQB == 16, "4, 8 or 16 heads per block");
@@ -392,9 +400,9 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   asm volatile("" : "+v"(fp16_magic));
 
 
-  auto key_is_m3 = [&](const PageMeta& m) -> bool {
+  auto key_is_m3 = [&](const PageMeta& m, auto fm) -> bool {
     if constexpr (KMODE == KEYS_M3) return true;
-    if constexpr (KMODE == KEYS_M0) return false;
+    if constexpr (KMODE == KEYS_M0 || decltype(fm)::value) return false;
     return m.kfmt == DC_FMT_M3_F16;
   };
 
@@ -426,26 +434,39 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // The row's bits split into RPI i and l / PPR, so the lane's offset is
   // kdma0 ^ 16 key_swz(RPI i): one register per distinct swizzle constant.
   constexpr int PPR = HD / 8, RPI = 64 / PPR, NDMA = 32 / RPI;
-  const uint32_t kdma0 = uint32_t(lane / PPR) * PPR * 16 + 16u * (uint32_t(lane % PPR) ^ key_swz<PPR>(lane / PPR));
-  // (equal swizzle constants give equal values, which share a register; a
-  // literal bound: hipcc's host pass drops the kernel stubs when this array's
-  // size is a dependent constant)
   static_assert(NDMA <= 16, "at most 16 DMA instructions per chunk");
-  uint32_t kdma[16];
-#pragma unroll
-  for (int i = 0; i < NDMA; ++i) kdma[i] = kdma0 ^ (16u * key_swz<PPR>(uint32_t(RPI * i)));
+  auto dma_off = [](uint32_t l, int i) -> uint32_t {
+    const uint32_t base = (l / PPR) * PPR * 16 + 16u * ((l % PPR) ^ key_swz<PPR>(l / PPR));
+    return base ^ (16u * key_swz<PPR>(uint32_t(RPI * i)));
+  };
   // score read of tile hh, group g: row ta = 8 (r / 4) + 4 hh + r % 4, piece
   // 4 g + kb at slot (4 g + kb) ^ key_swz(ta); key_swz(ta) < 16, so group g
-  // reads krd[hh][g % 4] + 64 (g / 4) words
-  constexpr int KJ = KG < 4 ? KG : 4;
-  uint32_t krd[2][KJ];
+  // reads krd_off(hh, g % 4) + 64 (g / 4) words
+  auto krd_off = [](uint32_t l, int hh, int j) -> uint32_t {
+    const uint32_t rr = l & 15u, ta = 8 * (rr >> 2) + 4 * hh + (rr & 3);
+    return ta * (HD / 2) + 4u * ((uint32_t(4 * j) + (l >> 4)) ^ key_swz<PPR>(ta));  // in words
+  };
+  // M3-only key pools read LDS keys every chunk: their offsets are computed
+  // once (equal swizzle constants give equal values, which share a
+  // register; literal bounds: hipcc's host pass drops the kernel stubs when
+  // such an array's size is a dependent constant).  Other pools meet M3
+  // chunks rarely and derive the offsets where they are used, from a lane
+  // index the compiler cannot hoist, so none of them stays live across the
+  // chunk loop.
+  uint32_t kdma[16], krd[2][4];
+  if constexpr (KMODE == KEYS_M3) {
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
+    for (int i = 0; i < NDMA; ++i) kdma[i] = dma_off(uint32_t(lane), i);
 #pragma unroll
-    for (int j = 0; j < KJ; ++j) {
-      const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
-      krd[hh][j] = ta * (HD / 2) + 4u * (uint32_t(4 * j + kb) ^ key_swz<PPR>(ta));  // in words
-    }
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int j = 0; j < (KG < 4 ? KG : 4); ++j) krd[hh][j] = krd_off(uint32_t(lane), hh, j);
+  }
+  auto fresh_lane = []() __attribute__((always_inline)) -> uint32_t {
+    uint32_t l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(l));
+    return l;
+  };
   uint32_t voff[Cfg::NVP];
 #pragma unroll
   for (int k = 0; k < Cfg::NVP; ++k) {
@@ -455,13 +476,22 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   }
   const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
-  auto load_chunk = [&](const PageMeta& m, Regs& R, auto kbi) __attribute__((always_inline)) {
+  auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi, auto fm) __attribute__((always_inline)) {
+    constexpr bool M0O = decltype(fm)::value;
+    constexpr int KM = M0O ? KEYS_M0 : KMODE;
+    constexpr bool ROWS = kRowRegs && !M0O;
     const int c0 = m.c0;
     auto dma_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
+      const uint32_t l = KMODE == KEYS_M3 ? 0u : fresh_lane();
 #pragma unroll
-      for (int i = 0; i < NDMA; ++i)
+      for (int i = 0; i < NDMA; ++i) {
+        // (the offset goes to the builtin as a plain variable: hipcc's host
+        // pass drops the kernel stubs when this argument is an expression
+        // with a call or an array element of a dependent size)
+        const uint32_t off = KMODE == KEYS_M3 ? kdma[i] : dma_off(l, i);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(kbuf(kbi) + 256 * i),
-                                                 16, kdma[i], c0 * HD * 2 + 1024 * i, 0, kNT);
+                                                 16, off, c0 * HD * 2 + 1024 * i, 0, kNT);
+      }
     };
     auto word_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
 #pragma unroll
@@ -488,11 +518,11 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(ksoff), kbs + c0 * KG * 2 + 256 * k, kNT);
       }
     };
-    if constexpr (kRowRegs) {
+    if constexpr (ROWS) {
       // both formats through the same loads (wave-uniform offsets), so every
       // chunk issues the same loads and the compiler's counts of loads in
       // flight stay exact across chunks of either format
-      const bool km3 = key_is_m3(m);
+      const bool km3 = key_is_m3(m, fm);
       const int cbase = c0 * (km3 ? HD * 2 : KBLK);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
@@ -510,11 +540,11 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         if constexpr (KAFF)
           R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), kbs + c0 * KG * 2 + 256 * k, kNT);
       }
-    } else if constexpr (KMODE == KEYS_M3) {
+    } else if constexpr (KM == KEYS_M3) {
       dma_keys(m.krs);
-    } else if constexpr (KMODE == KEYS_M0) {
+    } else if constexpr (KM == KEYS_M0) {
       word_keys(m.krs);
-    } else if (key_is_m3(m)) {  // one chunk in flight: a wave-uniform branch
+    } else if (key_is_m3(m, fm)) {  // one chunk in flight: a wave-uniform branch
       dma_keys(m.krs);
     } else {
       word_keys(m.krs);
@@ -532,7 +562,8 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- registers -> an LDS stage buffer: value codes in padded rows, scales as loaded ([32][G] fp16) ----
-  auto stage_chunk = [&](const Regs& R, uint32_t* lds) __attribute__((always_inline)) {
+  auto stage_chunk = [&](const auto& R, uint32_t* lds, auto fm) __attribute__((always_inline)) {
+    constexpr int KM = decltype(fm)::value ? KEYS_M0 : KMODE;
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k) {
       const int e = lane + 64 * k;
@@ -561,7 +592,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
         if constexpr (VAFF) put(lds + Cfg::VBS, R.vb[k], e, VG);
       }
     }
-    if constexpr (KMODE != KEYS_M3) {
+    if constexpr (KM != KEYS_M3) {
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
         const int e = lane + 64 * k;
@@ -574,14 +605,19 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   };
 
   // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
-  auto score_chunk = [&](const PageMeta& m, const Regs& R, const uint32_t* lds, auto kbi, float* Ls) __attribute__((always_inline)) {
+  auto score_chunk = [&](const PageMeta& m, const auto& R, const uint32_t* lds, auto kbi, float* Ls,
+                         auto fm) __attribute__((always_inline)) {
+    constexpr bool M0O = decltype(fm)::value;
+    constexpr int KM = M0O ? KEYS_M0 : KMODE;
+    constexpr bool ROWS = kRowRegs && !M0O, DMAK = kDmaK && !M0O;
     const uint32_t* kl = kbuf(kbi);
     // MFMA results are read a few instructions after issue only at the very
     // end: the M3 paths keep four independent accumulation chains (token
     // tile hh x high / residual query part), the M0 path scales group g - 1
     // while the MFMAs of group g run
-    if (key_is_m3(m)) {
-      if constexpr (kDmaK || kRowRegs) {
+    if (key_is_m3(m, fm)) {
+      if constexpr (DMAK || ROWS) {
+        const uint32_t l3 = KMODE == KEYS_M3 || ROWS ? 0u : fresh_lane();
         f32x4 dh[2], dl[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) dh[hh] = dl[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -592,10 +628,12 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           for (int hh = 0; hh < 2; ++hh) {
             // channels (0, 1), (2, 3), (4, 5), (6, 7) of the lane's 8
             u32x4 x;
-            if constexpr (kRowRegs)
+            if constexpr (ROWS)
               x = R.kr[hh][g];
-            else
+            else if constexpr (KMODE == KEYS_M3)
               x = *reinterpret_cast<const u32x4*>(kl + krd[hh][g % 4] + 64 * (g / 4));
+            else
+              x = *reinterpret_cast<const u32x4*>(kl + krd_off(l3, hh, g % 4) + 64 * (g / 4));
             if constexpr (kPairedQ) {  // -> (0, 4), (1, 5), (2, 6), (3, 7)
               ka[hh].u[0] = __builtin_amdgcn_perm(x.z, x.x, 0x05040100u);
               ka[hh].u[1] = __builtin_amdgcn_perm(x.z, x.x, 0x07060302u);
@@ -615,7 +653,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = dh[hh][i] + dl[hh][i];
       }
-    } else if constexpr (KMODE != KEYS_M3) {  // M0 4- or 8-bit, group 32: scale and bias per group in fp32
+    } else if constexpr (KM != KEYS_M3) {  // M0 4- or 8-bit, group 32: scale and bias per group in fp32
       // affine: codes n, bias b; symmetric: codes n - (2^(KBITS-1) - 1), no
       // bias (bf = 0 zeroes the bias words, which then alias the scales)
       const bool k_affine = KAFF && m.kfmt == DC_FMT_M0_AFFINE;
@@ -703,7 +741,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           for (int hh = 0; hh < 2; ++hh) {
             if constexpr (KBITS == 4) {
               uint32_t w;
-              if constexpr (kRowRegs) {
+              if constexpr (ROWS) {
                 const u32x4 x = R.kr[hh][g];
                 w = hh == 1 && last_row ? x.w : x.x;
               } else {
@@ -724,7 +762,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
               // pair (1024 + n_2j, 1024 + n_2j+1), and one packed add makes
               // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
               uint32_t wa, wb;
-              if constexpr (kRowRegs) {
+              if constexpr (ROWS) {
                 const u32x4 x = R.kr[hh][g];
                 wa = hh == 1 && last_row ? x.z : x.x;
                 wb = hh == 1 && last_row ? x.w : x.y;
@@ -812,9 +850,10 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   // same overflow margin: weight x scale x 16 reaches fp16's maximum only
   // for 8-bit scales above 1023).  The epilogue divides by kVS.
   constexpr float kVS = VBITS == 8 ? 16.f : 1.f;
-  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa) __attribute__((always_inline)) {
+  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa, auto fm) __attribute__((always_inline)) {
+    constexpr bool VM3E = VM3 && !decltype(fm)::value;
     bool v_m0 = true;
-    if constexpr (VM3) v_m0 = is_m0(m.vfmt);
+    if constexpr (VM3E) v_m0 = is_m0(m.vfmt);
     if (v_m0) {
       const bool v_affine = VAFF && m.vfmt == DC_FMT_M0_AFFINE;
       const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
@@ -911,7 +950,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
           }
         }
       }
-    } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): rows staged in vbuf
+    } else if constexpr (VM3E) {  // M3 fp16 values (the exact recent window): rows staged in vbuf
       Frag fa_hi, fa_res;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
@@ -924,16 +963,18 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       // key_swz(t).  A token at or past the page's count reads 0 (its
       // weight is 0, and the row's bytes need not be finite).
       const uint16_t* V = reinterpret_cast<const uint16_t*>(vbuf);
-      const int tvalid = m.T - m.c0 - 8 * kb;  // tokens 8 kb + e with e < tvalid are valid
+      const uint32_t l = fresh_lane(), kbv = l >> 4, rv = l & 15u;
+      const uint32_t dcolv = 8 * (rv / LPW4) + rv % LPW4;
+      const int tvalid = m.T - m.c0 - 8 * int(kbv);  // tokens 8 kb + e with e < tvalid are valid
 #pragma unroll
       for (int g = 0; g < VG; ++g)
 #pragma unroll
         for (int h = 0; h < H; ++h) {
-          const uint32_t d = uint32_t(VGS * g + dcol + LPW4 * h);
+          const uint32_t d = uint32_t(VGS * g + LPW4 * h) + dcolv;
           Frag fb;
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t t0 = uint32_t(8 * kb + 2 * pp), t1 = t0 + 1;
+            const uint32_t t0 = 8 * kbv + uint32_t(2 * pp), t1 = t0 + 1;
             uint32_t lo = V[t0 * HD + 8 * ((d >> 3) ^ key_swz<PPR>(t0)) + (d & 7)];
             uint32_t hi = V[t1 * HD + 8 * ((d >> 3) ^ key_swz<PPR>(t1)) + (d & 7)];
             if (2 * pp >= tvalid) lo = 0;
@@ -950,10 +991,13 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   auto load_value_rows = [&](const PageMeta& m) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rows =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0, m.T * HD * 2, 0x00020000);
+    const uint32_t l = fresh_lane();
 #pragma unroll
-    for (int i = 0; i < NDMA; ++i)
+    for (int i = 0; i < NDMA; ++i) {
+      const uint32_t off = dma_off(l, i);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rows, (__attribute__((address_space(3))) void*)(vbuf + 256 * i), 16,
-                                               kdma[i], m.c0 * HD * 2 + 1024 * i, 0, kNT);
+                                               off, m.c0 * HD * 2 + 1024 * i, 0, kNT);
+    }
   };
 
   // head_dim 256 converts up front: holding its raw queries across the first
@@ -1034,65 +1078,80 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       return m;
     };
 
-    if constexpr (kPipe) {
-      // chunk j is mixed from stage buffer j % 2 while chunk j + 1 is staged
-      // into the other buffer and scored, and the loads of chunk j + 2 fly
-      // into the register set chunk j + 1 came in; past the last chunk the
-      // loads go to an empty resource (no memory traffic)
-      uint32_t* const buf0 = lds_all;
-      uint32_t* const buf1 = lds_all + Cfg::STAGE;
-      Regs RA, RB;
-      PageMeta cur = chunk_meta(0);
-      PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
-      load_chunk(cur, RA, KB0{});
-      load_chunk(nxt, RB, KB1{});
-      prep_queries();
-      float Ls[8], pa[8];
-      stage_chunk(RA, buf0);
-      score_chunk(cur, RA, buf0, KB0{}, Ls);
-      softmax_chunk(cur, Ls, pa);
-      int j = 0;
-      // chunk j: values in stage buffer bm (keys in km, already scored);
-      // chunk j + 1: registers X, keys in ks; chunk j + 2 loads into Y, km
-      auto step = [&](Regs& X, Regs& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) __attribute__((always_inline)) -> bool {
-        if (j + 1 >= total) {  // last chunk: mix only
-          mix_chunk(cur, bm, pa);
-          return false;
-        }
-        const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : no_chunk(nxt);
-        load_chunk(n2, Y, km);
-        float Ln[8];
-        stage_chunk(X, bs);
-        score_chunk(nxt, X, bs, ks, Ln);
-        mix_chunk(cur, bm, pa);
-        softmax_chunk(nxt, Ln, pa);
-        cur = nxt;
-        nxt = n2;
-        ++j;
-        return true;
-      };
-      while (step(RB, RA, buf0, buf1, KB0{}, KB1{}) && step(RA, RB, buf1, buf0, KB1{}, KB0{})) {
-      }
-    } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
-      // (M3 value rows go to vbuf once the previous chunk's mix has read it)
-      Regs R;
-      PageMeta cur = chunk_meta(0);
-      load_chunk(cur, R, KB0{});
-      if constexpr (VM3)
-        if (!is_m0(cur.vfmt)) load_value_rows(cur);
-      prep_queries();
-      for (int j = 0; j < total; ++j) {
-        const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
+    auto run = [&](auto fm) __attribute__((always_inline)) {
+      using R_t = ChunkRegs<HD, VGS, VBITS, (decltype(fm)::value ? int(KEYS_M0) : KMODE), KBITS,
+                            (kRowRegs && !decltype(fm)::value)>;
+      if constexpr (kPipe) {
+        // chunk j is mixed from stage buffer j % 2 while chunk j + 1 is staged
+        // into the other buffer and scored, and the loads of chunk j + 2 fly
+        // into the register set chunk j + 1 came in; past the last chunk the
+        // loads go to an empty resource (no memory traffic)
+        uint32_t* const buf0 = lds_all;
+        uint32_t* const buf1 = lds_all + Cfg::STAGE;
+        R_t RA, RB;
+        PageMeta cur = chunk_meta(0);
+        PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
+        load_chunk(cur, RA, KB0{}, fm);
+        load_chunk(nxt, RB, KB1{}, fm);
+        prep_queries();
         float Ls[8], pa[8];
-        stage_chunk(R, lds_all);
-        score_chunk(cur, R, lds_all, KB0{}, Ls);
-        load_chunk(nm, R, KB0{});
+        stage_chunk(RA, buf0, fm);
+        score_chunk(cur, RA, buf0, KB0{}, Ls, fm);
         softmax_chunk(cur, Ls, pa);
-        mix_chunk(cur, lds_all, pa);
-        if constexpr (VM3)
-          if (j + 1 < total && !is_m0(nm.vfmt)) load_value_rows(nm);
-        cur = nm;
+        int j = 0;
+        // chunk j: values in stage buffer bm (keys in km, already scored);
+        // chunk j + 1: registers X, keys in ks; chunk j + 2 loads into Y, km
+        auto step = [&](R_t& X, R_t& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) __attribute__((always_inline)) -> bool {
+          if (j + 1 >= total) {  // last chunk: mix only
+            mix_chunk(cur, bm, pa, fm);
+            return false;
+          }
+          const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : no_chunk(nxt);
+          load_chunk(n2, Y, km, fm);
+          float Ln[8];
+          stage_chunk(X, bs, fm);
+          score_chunk(nxt, X, bs, ks, Ln, fm);
+          mix_chunk(cur, bm, pa, fm);
+          softmax_chunk(nxt, Ln, pa);
+          cur = nxt;
+          nxt = n2;
+          ++j;
+          return true;
+        };
+        while (step(RB, RA, buf0, buf1, KB0{}, KB1{}) && step(RA, RB, buf1, buf0, KB1{}, KB0{})) {
+        }
+      } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
+        // (M3 value rows go to vbuf once the previous chunk's mix has read it)
+        constexpr bool VM3E = VM3 && !decltype(fm)::value;
+        R_t R;
+        PageMeta cur = chunk_meta(0);
+        load_chunk(cur, R, KB0{}, fm);
+        if constexpr (VM3E)
+          if (!is_m0(cur.vfmt)) load_value_rows(cur);
+        prep_queries();
+        for (int j = 0; j < total; ++j) {
+          const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
+          float Ls[8], pa[8];
+          stage_chunk(R, lds_all, fm);
+          score_chunk(cur, R, lds_all, KB0{}, Ls, fm);
+          load_chunk(nm, R, KB0{}, fm);
+          softmax_chunk(cur, Ls, pa);
+          mix_chunk(cur, lds_all, pa, fm);
+          if constexpr (VM3E)
+            if (j + 1 < total && !is_m0(nm.vfmt)) load_value_rows(nm);
+          cur = nm;
+        }
       }
+    };
+    if constexpr (kTwoLoops) {
+      // the batch's valid pages all hold M0 keys and values: the M0 loop
+      const uint64_t other = __ballot(T > 0 && !(km0 && vm0));
+      if (other == 0)
+        run(FM_M0{});
+      else
+        run(FM_ANY{});
+    } else {
+      run(FM_ANY{});
     }
   }
 
