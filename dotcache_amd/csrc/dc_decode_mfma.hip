@@ -1028,23 +1028,33 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     const uint32_t vtot = vm0 ? vpay + vsb + (vaff ? vsb : 0u) : m3_bytes;
     int T = min(int(k1 & 0xffff), int(v1 & 0xffff));
     T = min(T, CAP);
-    if (!ok || lane >= nb || (int64_t(k0) << 8) + ktot > a.kpool.arena_bytes ||
-        (int64_t(v0) << 8) + vtot > a.vpool.arena_bytes)
-      T = 0;
+    // (bitwise, not short-circuit: no branch)
+    const bool bad = !ok | (lane >= nb) | ((uint64_t(k0) << 8) + ktot > uint64_t(a.kpool.arena_bytes)) |
+                     ((uint64_t(v0) << 8) + vtot > uint64_t(a.vpool.arena_bytes));
+    if (bad) T = 0;
     const uint32_t info = uint32_t(T) | (uint32_t(kf) << 16) | (uint32_t(vf) << 24);
     const uint32_t koffs = ksc | (kbs << 16), voffs = vsc | (vbs << 16);  // offsets < 64 KiB for M0 pages
     const int nch = (T + 31) >> 5;  // < 16 (capacity <= 256)
-    // inclusive prefix sum over the lanes (end chunk of page lane), bit by
-    // bit: ballot of the bit, count of set lanes at or below this one
+    // end chunk of page lane (inclusive prefix sum over the lanes).  Every
+    // page of the batch full, with a power-of-two count of chunks per page
+    // (2^cps): page lane ends at chunk (lane + 1) 2^cps and chunk j lies in
+    // page j >> cps.  Otherwise bit by bit: ballot of the bit, count of set
+    // lanes at or below this one.
+    const int cpp = CAP >> 5, cps = __builtin_ctz(uint32_t(cpp));
+    const bool fast = __ballot(lane < nb && T != CAP) == 0 && (cpp & (cpp - 1)) == 0;
     int cend = 0;
+    if (fast) {
+      cend = (lane < nb ? lane + 1 : nb) << cps;
+    } else {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int bit = (nch >> b) & 1;
-      const uint64_t bal = __ballot(bit);
-      const int below = __builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u));
-      cend += (below + bit) << b;
+      for (int b = 0; b < 4; ++b) {
+        const int bit = (nch >> b) & 1;
+        const uint64_t bal = __ballot(bit);
+        const int below = __builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u));
+        cend += (below + bit) << b;
+      }
     }
-    const int total = __builtin_amdgcn_readlane(cend, 63);
+    const int total = fast ? nb << cps : __builtin_amdgcn_readlane(cend, 63);
     if (total == 0) continue;
     // chunk j lies in the first page whose end chunk exceeds j
     // a chunk past the end: the same loads against empty buffer resources,
@@ -1055,7 +1065,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       return m;
     };
     auto chunk_meta = [&](int j) __attribute__((always_inline)) -> PageMeta {
-      const int i = __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
+      const int i = fast ? j >> cps : __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
       PageMeta m;
       // blob pointers stay derived from the arena arguments (global memory)
       const uint8_t* kp =
@@ -1074,7 +1084,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       m.kbs = ko >> 16;
       m.vsc = vo & 0xffff;
       m.vbs = vo >> 16;
-      m.c0 = (j - (__builtin_amdgcn_readlane(cend, i) - ((m.T + 31) >> 5))) * 32;
+      m.c0 = fast ? (j & (cpp - 1)) * 32 : (j - (__builtin_amdgcn_readlane(cend, i) - ((m.T + 31) >> 5))) * 32;
       return m;
     };
 
