@@ -145,6 +145,40 @@ def test_fused_mixed_key_formats_per_page(kbits):
     np.testing.assert_allclose(got, want, atol=2e-4, rtol=0)
 
 
+@pytest.mark.parametrize("hd", [64, 128, 256])
+@pytest.mark.parametrize("kbits", [4, 8])
+def test_fused_mixed_key_and_value_formats_every_head_dim(hd, kbits):
+    """M3 and M0 pages interleaved in both the key and the value lists, at
+    every head_dim the MFMA kernel takes, with a partial last page: the M3
+    key and value rows reach LDS by DMA in their slot swizzle (3 bits at
+    head_dim 64, 4 above) and the rows past the page's tokens must not
+    contribute.  Compared at the kernels' tolerance, with automatic head
+    blocks and with blocks of 16."""
+    from dotcache_amd.backends import decode_grouped_multiquery_step_prepared_hip_tensor_output_only as fused
+    from dotcache_amd.decode import set_decode_path, set_mfma_head_block
+
+    set_decode_path("mfma")
+    rng = np.random.default_rng(900 + hd + kbits)
+    tpp, n, Q = 64, 9 * 64 - 23, 4
+    keys = hard_values(rng, n, hd)
+    vals = hard_values(rng, n, hd)
+    kp, vp = [], []
+    for i, s in enumerate(range(0, n, tpp)):
+        kf = dict(mode="M3") if i % 3 == 2 else dict(bits=kbits, scheme="affine" if i % 2 else "symmetric")
+        vf = dict(mode="M3") if i % 4 in (1, 3) or s + tpp >= n else dict(bits=4, scheme="affine")
+        kp.append(O.encode_page(keys[s:s + tpp], head_dim=hd, group_size=32, kind="K", token_start=s, **kf))
+        vp.append(O.encode_page(vals[s:s + tpp], head_dim=hd, group_size=32, kind="V", token_start=s, **vf))
+    q = (rng.normal(size=(1, Q, hd)) / np.sqrt(hd)).astype(np.float32)
+    want = O.decode_grouped(q, [kp], [vp])
+    args = (list(q), [[to_product_page(p) for p in kp]], [[to_product_page(p) for p in vp]])
+    for nqb in (0, 16):
+        set_mfma_head_block(nqb)
+        for pps in (None, 2):
+            got = fused(*args, pages_per_split=pps).cpu().numpy()
+            err = np.max(np.abs(got - want))
+            assert err < KERNEL_TOL, f"head block {nqb} pps {pps}: max-abs error {err}"
+
+
 def test_four_and_eight_bit_keys_in_one_pool_take_the_generic_kernel():
     """The MFMA kernel takes one key code width per launch: a pool holding
     both runs on the generic kernel under "auto", and path "mfma" refuses it."""
