@@ -353,17 +353,35 @@ def main():
     # as a graph of one step's launches (unless --eager), so that a short
     # kernel is not timed at the host's launch rate; medians over >= 50
     # replays, an event between replays
-    def decode_all():
-        for l in range(L):
+    # (the KV sets are cycled here as in the steps, so every launch reads
+    # its pages from HBM)
+    R = wl.replicas
+
+    def decode_set(r):
+        for l in wl.replica_layers(r):
             wl.decode_kernel(l)
 
-    def merge_all():
-        for l in range(L):
+    def merge_set(r):
+        for l in wl.replica_layers(r):
             wl.merge_kernel(l)
 
-    if not args.eager:
-        g_dec, g_merge = wl.capture_fn(decode_all), wl.capture_fn(merge_all)
-        decode_all, merge_all = g_dec.replay, g_merge.replay
+    if args.eager:
+        dec_fns = [lambda r=r: decode_set(r) for r in range(R)]
+        merge_fns = [lambda r=r: merge_set(r) for r in range(R)]
+    else:
+        dec_fns = [wl.capture_fn(lambda r=r: decode_set(r)).replay for r in range(R)]
+        merge_fns = [wl.capture_fn(lambda r=r: merge_set(r)).replay for r in range(R)]
+
+    def cycling(fns):
+        turn = [0]
+
+        def call():
+            fns[turn[0] % len(fns)]()
+            turn[0] += 1
+
+        return call
+
+    decode_all, merge_all = cycling(dec_fns), cycling(merge_fns)
     dec_ms = per_call(decode_all, n_med) / L
     merge_ms_all = per_call(merge_all, n_med) / L
     # roofline.achieved uses the mean launch time (what a kernel trace's
@@ -410,6 +428,7 @@ def main():
         "config": {
             "workload": spec.name,
             "layers": L,
+            "kv_sets": wl.replicas,
             "batch": spec.batch,
             "context": int(spec.context) if spec.ragged is None else f"log-uniform {spec.ragged}",
             "q_heads": spec.n_q_heads,

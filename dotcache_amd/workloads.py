@@ -56,6 +56,7 @@ class WorkloadSpec:
     outlier_channels: int = 0
     distribution: str = "normal"
     append: bool = False                   # per-step encode/append of the new token
+    replicas: int = 1                      # independent KV sets cycled step by step (working set past the MALL)
     description: str = ""
 
     @property
@@ -68,8 +69,9 @@ SPECS = {
                        PageFormat("M0", "symmetric", 4, 32), context=1024,
                        description="1 layer, 1 q / 1 kv head, hd 64, 16 pages, M0 symmetric 4-bit g32"),
     "c2": WorkloadSpec("c2_llama32_1b", 16, 32, 8, 64, 1, 64, PageFormat("M0", "affine", 4, 32),
-                       PageFormat("M0", "affine", 4, 32), context=4096,
-                       description="Llama-3.2-1B-shaped: 16 L, 32 q / 8 kv, hd 64, ctx 4096, M0 affine 4-bit g32"),
+                       PageFormat("M0", "affine", 4, 32), context=4096, replicas=8,
+                       description="Llama-3.2-1B-shaped: 16 L, 32 q / 8 kv, hd 64, ctx 4096, M0 affine 4-bit g32; "
+                                   "8 KV sets (336 MB) cycled step by step, past the 256 MB MALL"),
     "c3": WorkloadSpec("c3_qwen25_7b_gqa", 28, 28, 4, 128, 8, 64, PageFormat("M3"),
                        PageFormat("M0", "symmetric", 4, 32), context=16384, outlier_channels=4,
                        description="Qwen2.5-7B-shaped: 28 L, 28 q / 4 kv (GQA 7), hd 128, batch 8 x 16384, "
@@ -128,7 +130,8 @@ class Workload:
     k_page_ids_by_layer: list = field(default_factory=list)
     v_page_ids_by_layer: list = field(default_factory=list)
     attended: np.ndarray | None = None
-    graph: object = None  # captured HIP graph of one whole step
+    graph: object = None  # captured HIP graphs of one whole step, one per replica
+    next_replica: int = 0
     tail_k_dev: list = field(default_factory=list)
     tail_v_dev: list = field(default_factory=list)
     slot_dev: object = None
@@ -137,12 +140,21 @@ class Workload:
     def query_scale(self) -> float:
         return 1.0 / float(np.sqrt(self.spec.head_dim))
 
+    @property
+    def replicas(self) -> int:
+        return self.spec.replicas
+
+    def replica_layers(self, r: int) -> range:
+        """Layer indices of KV set ``r``: a step attends one set's layers."""
+        L = self.spec.n_layers
+        return range(r * L, (r + 1) * L)
+
     def algorithmic_bytes_per_step(self) -> int:
-        """Compressed bytes one decode step reads (all layers, all sequences):
-        codes + fp16 scales / biases + fp16 escape rows for valid tokens, plus
-        the two int32 page-table entries per page."""
+        """Compressed bytes one decode step reads (all layers of one KV set,
+        all sequences): codes + fp16 scales / biases + fp16 escape rows for
+        valid tokens, plus the two int32 page-table entries per page."""
         total = 0
-        for l, lt in enumerate(self.layers):
+        for l in self.replica_layers(0):
             total += self.k_pool.read_bytes(self.k_page_ids_by_layer[l])
             total += self.v_pool.read_bytes(self.v_page_ids_by_layer[l])
             total += 8 * len(self.k_page_ids_by_layer[l])
@@ -157,13 +169,19 @@ class Workload:
         return self.attended
 
     def step(self) -> None:
-        """One decode step: per layer, (append) + the fused decode kernel +
-        the split-K merge kernel.  Replays the captured graph when
-        :meth:`capture` has been called."""
+        """One decode step: per layer of the next KV set (round robin over
+        the replicas), (append) + the fused decode kernel + the split-K merge
+        kernel.  Replays that set's captured graph when :meth:`capture` has
+        been called."""
+        r = self.next_replica
+        self.next_replica = (r + 1) % self.replicas
         if self.graph is not None:
-            self.graph.replay()
+            self.graph[r].replay()
             return
-        for l in range(len(self.layers)):
+        self.step_replica(r)
+
+    def step_replica(self, r: int) -> None:
+        for l in self.replica_layers(r):
             self.decode_layer(l)
             self.merge_kernel(l)
 
@@ -191,7 +209,7 @@ class Workload:
         loop costs one host launch per step.  Pools, tables, plan and
         buffers must not be reallocated afterwards."""
         self.graph = None
-        self.graph = self.capture_fn(self.step)
+        self.graph = [self.capture_fn(lambda r=r: self.step_replica(r)) for r in range(self.replicas)]
 
     def capture_fn(self, fn):
         """``fn`` (a sequence of this workload's kernel launches) captured as
@@ -231,9 +249,12 @@ def _gen(shape, gen, dist: str, device):
 
 def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | None = None, batch: int | None = None,
                    context: int | None = None, pages_per_split: int | None = None,
-                   scatter_pages: bool = True, key_bits: int | None = None) -> Workload:
+                   scatter_pages: bool = True, key_bits: int | None = None,
+                   replicas: int | None = None) -> Workload:
     """Encode every layer's pages on the device and build its page tables.
-    ``layers`` / ``batch`` / ``context`` shrink the workload for tests;
+    ``layers`` / ``batch`` / ``context`` shrink the workload for tests (one
+    KV set unless ``replicas`` says otherwise); ``replicas`` sets the number
+    of independent KV sets the steps cycle through;
     ``scatter_pages=False`` keeps each sequence's pages in allocation order;
     ``key_bits`` re-codes the configuration's M0 key pages at that width
     (a variant named ``<workload>_k<bits>``)."""
@@ -250,7 +271,13 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
 
         spec = replace(spec, n_layers=layers or spec.n_layers, batch=batch or spec.batch,
                        context=context or spec.context,
-                       ragged=None if (context and spec.ragged) else spec.ragged)
+                       ragged=None if (context and spec.ragged) else spec.ragged, replicas=1)
+    if replicas is not None:
+        from dataclasses import replace
+
+        if int(replicas) < 1:
+            raise ValueError("replicas must be at least 1")
+        spec = replace(spec, replicas=int(replicas))
     dev = torch.device(device)
     B, H, Q, hd, P = spec.batch, spec.n_kv_heads, spec.gqa, spec.head_dim, spec.page_size
     lengths = context_lengths(spec, seed)
@@ -261,7 +288,8 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
     kgeo = PoolGeometry(hd, spec.key.group_size, P)
     vgeo = PoolGeometry(hd, spec.value.group_size, P)
     m3map = key_m3_map(spec, seed)
-    total_pages = int(n_pages.sum()) * H * spec.n_layers
+    n_sets = spec.n_layers * spec.replicas  # layer sets built: every layer of every replica
+    total_pages = int(n_pages.sum()) * H * n_sets
 
     def pool_bytes(fmt, geo):
         f, b = fmt
@@ -277,13 +305,13 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
     queries, new_k, new_v = [], [], []
     kids_by_layer, vids_by_layer = [], []
     attended = lengths.copy()
-    for l in range(spec.n_layers):
+    for l in range(n_sets):
         gen.manual_seed(seed * 1000 + l)
         kt = np.zeros((B, H, stride), dtype=np.int32)
         vt = np.zeros((B, H, stride), dtype=np.int32)
         layer_k_ids, layer_v_ids = [], []
         for h in range(H):
-            kfmt = PageFormat("M3") if m3map[l, h] else spec.key
+            kfmt = PageFormat("M3") if m3map[l % spec.n_layers, h] else spec.key
             nph = int(n_pages.sum())
             kid = k_pool.allocate(*kfmt.fmt, nph)
             vid = v_pool.allocate(*spec.value.fmt, nph)
@@ -359,7 +387,7 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
                   attended=attended)
     wl.plan = make_plan(tables[0].seq_pages, H, pages_per_split, device=dev)
     wl.workspace = torch.zeros(max(workspace_bytes(wl.plan, Q, hd), 16), dtype=torch.uint8, device=dev)
-    wl.outs = [torch.empty((B, H, Q, hd), dtype=torch.float32, device=dev) for _ in range(spec.n_layers)]
+    wl.outs = [torch.empty((B, H, Q, hd), dtype=torch.float32, device=dev) for _ in range(n_sets)]
     if spec.append:
         wl.tail_k_dev = [torch.from_numpy(t.tail_k.ravel().astype(np.int32)).to(dev) for t in tables]
         wl.tail_v_dev = [torch.from_numpy(t.tail_v.ravel().astype(np.int32)).to(dev) for t in tables]

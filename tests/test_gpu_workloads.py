@@ -130,3 +130,31 @@ def test_graph_replays_match_eager_steps(name, context):
         wl.step()  # eager work between replays
         torch.cuda.synchronize()
         wl.graph = graph
+
+
+def test_kv_sets_cycle_step_by_step():
+    """A workload with two KV sets: consecutive steps attend set 0, then set
+    1, each layer of each set matching the oracle; the captured graphs (one
+    per set) replay the eager outputs bit for bit, in the same order."""
+    import torch
+
+    from dotcache_amd.workloads import build_workload
+
+    wl = build_workload("c2", seed=7, layers=2, batch=1, context=300, pages_per_split=2, replicas=2)
+    assert wl.replicas == 2 and len(wl.layers) == 4 and list(wl.replica_layers(1)) == [2, 3]
+    wl.step()
+    wl.step()
+    torch.cuda.synchronize()
+    B, H = wl.spec.batch, wl.spec.n_kv_heads
+    for layer in range(4):
+        _check(wl, layer, [(b, h) for b in range(B) for h in range(H)])
+    want = [o.clone() for o in wl.outs]
+    wl.capture()
+    assert wl.next_replica == 0
+    for r in (0, 1, 0):
+        for o in wl.outs:
+            o.fill_(float("nan"))
+        wl.step()
+        torch.cuda.synchronize()
+        for l in wl.replica_layers(r):
+            assert torch.equal(wl.outs[l], want[l]), f"set {r} layer {l} differs from the eager step"
