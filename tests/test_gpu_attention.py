@@ -278,8 +278,22 @@ def test_fused_decode_peaked_attention_and_small_values():
     assert np.max(np.abs(got - want)) < 1e-3
 
 
+# Merge layouts: (counts, begins or None for in order, unused slots).  The
+# merge kernel takes partials [b c, (b + 1) c) for merge b without waiting
+# for the merge item when the partial slots are a multiple c of the merge
+# count, and checks that guess against the item: "uniform" is a right guess,
+# "divisible" and "permuted" wrong ones that must fall back.
+MERGE_LAYOUTS = {
+    "ragged": ([5, 1, 40, 3], None, 2),
+    "uniform": ([6, 6, 6, 6], None, 0),
+    "divisible": ([5, 1, 10, 8], None, 0),
+    "permuted": ([6, 6, 6, 6], [6, 0, 18, 12], 0),
+}
+
+
+@pytest.mark.parametrize("layout", list(MERGE_LAYOUTS))
 @pytest.mark.parametrize("hd", [128, 30])
-def test_lse_merge_matches_float64(hd):
+def test_lse_merge_matches_float64(hd, layout):
     """dc_lse_merge on hand-made partials (m, l, o), log2 domain: ragged
     counts, empty partials (m = -inf) and a merge whose partials are all
     empty.  head_dim 30 takes the one-channel-per-thread path."""
@@ -292,14 +306,14 @@ def test_lse_merge_matches_float64(hd):
 
     rng = np.random.default_rng(hd)
     B, H, Q = 2, 2, 3
-    counts = [5, 1, 40, 3]                  # (seq, kv_head) in row-major order
-    n_part = sum(counts) + 2                # two unused slots at the end
+    counts, begins, spare = MERGE_LAYOUTS[layout]  # (seq, kv_head) in row-major order
+    n_part = sum(counts) + spare
     part_o = rng.normal(size=(n_part, Q, hd)).astype(np.float32)
     m = (rng.normal(size=(n_part, Q)) * 8).astype(np.float32)
     l = rng.uniform(0.5, 40.0, size=(n_part, Q)).astype(np.float32)
-    m[2, 1] = -np.inf                       # an empty partial inside merge 0
+    m[2, 1] = -np.inf                       # an empty partial
     l[2, 1] = 0.0
-    begins = np.cumsum([0] + counts[:-1])
+    begins = np.cumsum([0] + counts[:-1]) if begins is None else np.array(begins)
     m[begins[3]:begins[3] + 3] = -np.inf    # merge 3: every partial empty
     l[begins[3]:begins[3] + 3] = 0.0
     ml = np.stack([m, l], axis=-1)
