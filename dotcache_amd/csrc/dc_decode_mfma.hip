@@ -6,13 +6,17 @@
 // value codes, all from the compressed page bytes.  At the end it writes the
 // normalised output (an item that covers its whole sequence) or a split-K
 // partial (m, l, o) for the merge kernel.  Accepted pages: keys M3 fp16 or
-// M0 4-bit (group 32, affine or symmetric); values M0 4- or 8-bit (group 32
-// or 64, affine or symmetric) or M3 fp16; up to 16 query heads per KV head.
-// Other formats take the generic kernel (dc_decode.hip).
+// M0 4- or 8-bit (group 32, affine or symmetric; one width per launch);
+// values M0 4- or 8-bit (group 32 or 64, affine or symmetric) or M3 fp16;
+// up to 16 query heads per KV head.  Other formats take the generic kernel
+// (dc_decode.hip).
 //
-// Pipeline (head_dim <= 128): while chunk j is mixed, chunk j + 1 is staged
-// and scored and chunk j + 2 is being loaded, so the score's MFMA chain, the
-// mix's unpacking and the loads of one wavefront overlap.
+// Pipeline (head_dim <= 128, pools without M3 values): while chunk j is
+// mixed, chunk j + 1 is staged and scored and chunk j + 2 is being loaded,
+// so the score's MFMA chain, the mix's unpacking and the loads of one
+// wavefront overlap.  Other pools keep one chunk in flight.  M3 key and
+// value rows reach LDS by DMA (buffer_load ... lds), except in pipelined
+// pools of mixed key formats, which load 16-byte key pieces into registers.
 //
 // Exactness.  Every MFMA operand is exact: escape rows are fp16 already,
 // codes minus zero point are small integers, and each fp32 operand (scaled
@@ -178,7 +182,7 @@ __device__ __forceinline__ constexpr uint32_t key_swz(uint32_t t) {
 // One chunk: the page it belongs to (wave-uniform, in SGPRs) and its first token.
 struct PageMeta {
   __amdgpu_buffer_rsrc_t krs, vrs;  // buffer resources of the key / value blobs
-  const uint8_t* vp;                // value blob (M3 value rows are gathered through it)
+  const uint8_t* vp;                // value blob (M3 value rows are loaded from it)
   int T;                            // tokens of the page
   int kfmt, vfmt;
   uint32_t ksc, kbs, vsc, vbs;  // byte offsets of scales / biases in the blobs (0 where absent)
