@@ -1,5 +1,7 @@
 // Library-level C ABI: error reporting, blob sizes and the host-side decode
 // planner.  Host code only (compiled as HIP for the shared hip runtime).
+#include <algorithm>
+#include <vector>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -108,6 +110,98 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
   *n_partials = np;
   if (ni > max_items || nm > max_merges)
     return dc::fail(DC_ESPACE, "dc_plan_decode: need %d items and %d merges", ni, nm);
+  return DC_OK;
+}
+
+int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t target_items,
+                        int32_t min_pages_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
+                        dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials,
+                        int32_t* largest_item) {
+  if (!seq_pages || n_seqs <= 0 || n_kv_heads <= 0 || target_items <= 0 || min_pages_per_split <= 0 || !n_items ||
+      !n_merges || !n_partials || !largest_item)
+    return dc::fail(DC_EINVAL, "dc_plan_decode_fill: bad arguments");
+  int32_t top = 1;
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    if (seq_pages[b] <= 0)
+      return dc::fail(DC_EINVAL, "decode requires at least one page (sequence %d has %d)", b, seq_pages[b]);
+    top = std::max(top, seq_pages[b]);
+  }
+  // (1) the smallest pages-per-split (at least min_pages_per_split) whose
+  // near-equal splits fit target_items
+  auto count = [&](int64_t per) {
+    int64_t c = 0;
+    for (int32_t b = 0; b < n_seqs; ++b) c += (seq_pages[b] + per - 1) / per;
+    return c * n_kv_heads;
+  };
+  int64_t lo = std::min<int64_t>(min_pages_per_split, top), hi = top;
+  if (count(hi) <= target_items) {
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) / 2;
+      if (count(mid) <= target_items)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+  }
+  std::vector<int32_t> splits(n_seqs);
+  int64_t used = 0;
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    splits[b] = int32_t((seq_pages[b] + hi - 1) / hi);
+    used += int64_t(splits[b]) * n_kv_heads;
+  }
+  // (2) the items left in the budget go, one sequence (all its heads) at a
+  // time, to the sequence with the largest items, while its items keep at
+  // least min_pages_per_split pages
+  for (;;) {
+    if (used + n_kv_heads > target_items) break;
+    // largest mean item pages[b] / splits[b] (compared exactly), ties to
+    // the longer sequence
+    int32_t best = -1;
+    for (int32_t b = 0; b < n_seqs; ++b) {
+      if (seq_pages[b] / (splits[b] + 1) < min_pages_per_split) continue;
+      if (best < 0) {
+        best = b;
+        continue;
+      }
+      const int64_t lhs = int64_t(seq_pages[b]) * splits[best], rhs = int64_t(seq_pages[best]) * splits[b];
+      if (lhs > rhs || (lhs == rhs && seq_pages[b] > seq_pages[best])) best = b;
+    }
+    if (best < 0) break;
+    ++splits[best];
+    used += n_kv_heads;
+  }
+  int32_t ni = 0, nm = 0, np = 0, largest = 0;
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    const int32_t pages = seq_pages[b], sp = splits[b];
+    for (int32_t h = 0; h < n_kv_heads; ++h) {
+      const int32_t first_partial = np;
+      for (int32_t s = 0; s < sp; ++s) {
+        const int32_t pb = int32_t(int64_t(s) * pages / sp), pe = int32_t(int64_t(s + 1) * pages / sp);
+        largest = std::max(largest, pe - pb);
+        if (items && ni < max_items) {
+          dc_work_item& it = items[ni];
+          it.seq = b;
+          it.kv_head = h;
+          it.page_begin = pb;
+          it.page_end = pe;
+          it.partial = sp > 1 ? np : -1;
+          it.reserved[0] = it.reserved[1] = it.reserved[2] = 0;
+        }
+        ++ni;
+        if (sp > 1) ++np;
+      }
+      if (sp > 1) {
+        if (merges && nm < max_merges) merges[nm] = dc_merge_item{b, h, first_partial, sp};
+        ++nm;
+      }
+    }
+  }
+  *n_items = ni;
+  *n_merges = nm;
+  *n_partials = np;
+  *largest_item = largest;
+  if (ni > max_items || nm > max_merges)
+    return dc::fail(DC_ESPACE, "dc_plan_decode_fill: need %d items and %d merges", ni, nm);
   return DC_OK;
 }
 

@@ -122,28 +122,47 @@ def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items:
     return int(lo)
 
 
-def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *, device="cuda") -> DecodePlan:
+def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *, device="cuda",
+              target_items: int | None = None) -> DecodePlan:
+    """Work and merge items for a batch with these page counts.  With
+    ``pages_per_split`` the near-equal splits of ``dc_plan_decode``; without
+    it ``dc_plan_decode_fill``: the smallest such split that fits
+    ``target_items`` (default: one item per SIMD), then the rest of that
+    budget spent on further splits of the sequences with the largest items.
+    ``DecodePlan.pages_per_split`` is the largest item's page count."""
     torch = _torch()
     sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
     if sp.ndim != 1 or sp.size == 0:
         raise ValueError("seq_pages must be a non-empty 1-D array")
     if np.any(sp <= 0):
         raise ValueError("decode requires at least one page per sequence")
-    pps = choose_pages_per_split(sp, n_kv_heads) if pages_per_split is None else int(pages_per_split)
-    key = (sp.tobytes(), int(n_kv_heads), pps, str(device))
+    fill = pages_per_split is None
+    pps = 0 if fill else int(pages_per_split)
+    target = (int(target_items) if target_items else default_target_items()) if fill else 0
+    key = (sp.tobytes(), int(n_kv_heads), pps, target, str(device))
     hit = _plan_cache.get(key)
     if hit is not None:
         return hit
     L = _lib.lib()
-    ni, nm, npart = C.c_int32(), C.c_int32(), C.c_int32()
-    st = L.dc_plan_decode(sp.ctypes.data, sp.size, n_kv_heads, pps, None, 0, C.byref(ni), None, 0, C.byref(nm), C.byref(npart))
+    ni, nm, npart, big = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
+
+    def plan(items_p, max_items, merges_p, max_merges):
+        if fill:
+            return L.dc_plan_decode_fill(sp.ctypes.data, sp.size, n_kv_heads, target, MIN_PAGES_PER_SPLIT, items_p,
+                                         max_items, C.byref(ni), merges_p, max_merges, C.byref(nm), C.byref(npart),
+                                         C.byref(big))
+        return L.dc_plan_decode(sp.ctypes.data, sp.size, n_kv_heads, pps, items_p, max_items, C.byref(ni), merges_p,
+                                max_merges, C.byref(nm), C.byref(npart))
+
+    st = plan(None, 0, None, 0)
     if st not in (_lib.DC_OK, _lib.DC_ESPACE):
         _lib.check(st, "dc_plan_decode")
     items = (_lib.WorkItem * max(ni.value, 1))()
     merges = (_lib.MergeItem * max(nm.value, 1))()
-    st = L.dc_plan_decode(sp.ctypes.data, sp.size, n_kv_heads, pps, C.addressof(items), ni.value, C.byref(ni),
-                          C.addressof(merges), nm.value, C.byref(nm), C.byref(npart))
+    st = plan(C.addressof(items), ni.value, C.addressof(merges), nm.value)
     _lib.check(st, "dc_plan_decode")
+    if fill:
+        pps = int(big.value)
     host_items = np.frombuffer(bytes(items), dtype=np.int32).reshape(-1, 8)[: ni.value].copy()
     host_merges = np.frombuffer(bytes(merges), dtype=np.int32).reshape(-1, 4)[: nm.value].copy()
     dev_items = torch.frombuffer(bytearray(bytes(items)), dtype=torch.uint8).to(device)

@@ -256,6 +256,21 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
                    dc_work_item* items, int32_t max_items, int32_t* n_items,
                    dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials);
 
+/* Host-only planner that fills a launch: the near-equal splits of
+ * dc_plan_decode with the smallest pages-per-split (at least
+ * min_pages_per_split) that keeps n_kv_heads x sum(splits) <= target_items,
+ * then, while the budget allows, one more split (for all heads) of the
+ * sequence whose items are largest, as long as its items keep at least
+ * min_pages_per_split pages.  target_items is normally one item per SIMD.
+ * Same items, merges and DC_ESPACE convention as dc_plan_decode; *largest_item
+ * receives the largest item's page count.  The chunking of the reference's
+ * grouped decode (dotcache/backends/torch_mps.py:4110-4273) has no launch
+ * to fill; this planner has no reference counterpart beyond it. */
+int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t target_items,
+                        int32_t min_pages_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
+                        dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials,
+                        int32_t* largest_item);
+
 /* Fused decode attention straight from compressed pages: for every work
  * item, score its pages for the n_q GQA query heads of its KV head, take a
  * single-pass online softmax, and mix the value pages; then merge split-K

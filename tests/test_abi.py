@@ -77,6 +77,74 @@ def test_planner_covers_every_page_once():
     assert sorted(ms) == [(0, 0, 0, 2), (0, 1, 2, 2), (2, 0, 4, 3), (2, 1, 7, 3)]
 
 
+def _plan_fill(seq_pages, heads, target, min_pages=2):
+    sp = np.asarray(seq_pages, dtype=np.int32)
+    L = _lib.lib()
+    ni, nm, npart, big = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
+    st = L.dc_plan_decode_fill(sp.ctypes.data, sp.size, heads, target, min_pages, None, 0, C.byref(ni), None, 0,
+                               C.byref(nm), C.byref(npart), C.byref(big))
+    if st != _lib.DC_ESPACE:
+        _lib.check(st, "plan fill")
+    items = (_lib.WorkItem * max(ni.value, 1))()
+    merges = (_lib.MergeItem * max(nm.value, 1))()
+    st = L.dc_plan_decode_fill(sp.ctypes.data, sp.size, heads, target, min_pages, C.addressof(items), ni.value,
+                               C.byref(ni), C.addressof(merges), nm.value, C.byref(nm), C.byref(npart), C.byref(big))
+    _lib.check(st, "plan fill")
+    its = [(i.seq, i.kv_head, i.page_begin, i.page_end, i.partial) for i in items[: ni.value]]
+    ms = [(m.seq, m.kv_head, m.partial_begin, m.count) for m in merges[: nm.value]]
+    return its, ms, npart.value, big.value
+
+
+def _check_plan_shape(its, ms, npart, seq_pages, heads):
+    """Every (sequence, head) covers its pages once, in order, by near-equal
+    items; split streams own consecutive partial slots named by their merge."""
+    for b, n in enumerate(seq_pages):
+        for h in range(heads):
+            mine = [(pb, pe, part) for (s, hh, pb, pe, part) in its if s == b and hh == h]
+            assert [p for (pb, pe, _) in mine for p in range(pb, pe)] == list(range(n))
+            sizes = [pe - pb for (pb, pe, _) in mine]
+            assert max(sizes) - min(sizes) <= 1
+            if len(mine) == 1:
+                assert mine[0][2] == -1
+            else:
+                (m,) = [m for m in ms if m[0] == b and m[1] == h]
+                assert m[3] == len(mine) and [part for (_, _, part) in mine] == list(range(m[2], m[2] + m[3]))
+    assert npart == sum(m[3] for m in ms)
+
+
+def test_fill_planner_uses_the_whole_budget():
+    """C5's shape (4 x 4 streams of 1025 pages, one item per SIMD): the
+    page-count split leaves 976 items (17 pages); the fill planner spends the
+    other 48 on three more splits per stream, 64 items of 16 or 17 pages."""
+    its, ms, npart, big = _plan_fill([1025] * 4, 4, 1024)
+    assert len(its) == 1024 and big == 17 and len(ms) == 16 and all(m[3] == 64 for m in ms)
+    _check_plan_shape(its, ms, npart, [1025] * 4, 4)
+    # C3's shape already fills the budget: the plan of dc_plan_decode with 8 pages per split
+    its, ms, npart, big = _plan_fill([256] * 8, 4, 1024)
+    assert len(its) == 1024 and big == 8 and all(pe - pb == 8 for (_, _, pb, pe, _) in its)
+
+
+def test_fill_planner_ragged_and_limits():
+    rng = np.random.default_rng(11)
+    pages = rng.integers(1, 300, size=20).tolist()
+    its, ms, npart, big = _plan_fill(pages, 2, 100)
+    assert len(its) <= 100
+    _check_plan_shape(its, ms, npart, pages, 2)
+    # no split item below the minimum page count
+    assert all(pe - pb >= 2 for (s, _, pb, pe, part) in its if part >= 0)
+    # never a larger item than the smallest page-count split that fits
+    from dotcache_amd.decode import choose_pages_per_split
+
+    assert big <= choose_pages_per_split(np.asarray(pages), 2, target_items=100)
+    # more streams than the budget: one item per stream, over the target
+    its, ms, npart, big = _plan_fill([3] * 10, 2, 8)
+    assert len(its) == 20 and not ms and big == 3
+    with pytest.raises(ValueError):
+        _plan_fill([3, 0], 1, 8)
+    with pytest.raises(ValueError):  # no item budget
+        _plan_fill([3], 1, 0)
+
+
 def test_planner_rejects_empty_sequence():
     with pytest.raises(ValueError):
         _plan([3, 0], 1, 2)
