@@ -42,7 +42,7 @@ def format_bit(fmt: int, bits: int) -> int:
 class WorkItem(C.Structure):
     _fields_ = [
         ("seq", C.c_int32), ("kv_head", C.c_int32), ("page_begin", C.c_int32), ("page_end", C.c_int32),
-        ("partial", C.c_int32), ("reserved", C.c_int32 * 3),
+        ("partial", C.c_int32), ("chunk_begin", C.c_int32), ("chunk_end", C.c_int32), ("reserved", C.c_int32),
     ]
 
 
@@ -77,9 +77,9 @@ SIGNATURES = {
     "dc_select_top_k": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
     "dc_plan_decode": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.POINTER(C.c_int32),
                                  C.c_void_p, C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
-    "dc_plan_decode_fill": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int32,
-                                      C.POINTER(C.c_int32), C.c_void_p, C.c_int32, C.POINTER(C.c_int32),
-                                      C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "dc_plan_decode_fill": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int64, C.c_int32,
+                                      C.c_int32, C.c_void_p, C.c_int32, C.POINTER(C.c_int32), C.c_void_p, C.c_int32,
+                                      C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "dc_decode_paged": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
                                   C.c_void_p, C.c_int32, C.c_float, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                   C.c_void_p, C.c_int64, C.c_void_p]),

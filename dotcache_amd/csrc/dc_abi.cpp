@@ -1,6 +1,8 @@
 // Library-level C ABI: error reporting, blob sizes and the host-side decode
 // planner.  Host code only (compiled as HIP for the shared hip runtime).
 #include <algorithm>
+#include <cmath>
+#include <cstdint>
 #include <vector>
 #include <cstdarg>
 #include <cstdio>
@@ -45,7 +47,7 @@ extern "C" {
 
 const char* dc_last_error(void) { return dc::g_last_error; }
 
-int32_t dc_abi_version(void) { return 1; }
+int32_t dc_abi_version(void) { return 2; }
 
 int64_t dc_page_blob_bytes(int32_t format, int32_t bits, dc_page_geometry geometry) {
   if (!dc::valid_format(format, bits) || dc::validate_geometry(geometry) != DC_OK) return -1;
@@ -94,7 +96,7 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
           it.page_begin = int32_t(int64_t(s) * pages / splits);
           it.page_end = int32_t(int64_t(s + 1) * pages / splits);
           it.partial = splits > 1 ? np : -1;
-          it.reserved[0] = it.reserved[1] = it.reserved[2] = 0;
+          it.chunk_begin = it.chunk_end = it.reserved = 0;
         }
         ++ni;
         if (splits > 1) ++np;
@@ -113,87 +115,113 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
   return DC_OK;
 }
 
-int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t target_items,
-                        int32_t min_pages_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
+int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t chunks_per_page,
+                        const float* page_cost, int64_t cost_stride, int32_t target_items,
+                        int32_t min_chunks_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
                         dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials,
                         int32_t* largest_item) {
-  if (!seq_pages || n_seqs <= 0 || n_kv_heads <= 0 || target_items <= 0 || min_pages_per_split <= 0 || !n_items ||
-      !n_merges || !n_partials || !largest_item)
+  if (!seq_pages || n_seqs <= 0 || n_kv_heads <= 0 || chunks_per_page <= 0 || target_items <= 0 ||
+      min_chunks_per_split <= 0 || !n_items || !n_merges || !n_partials || !largest_item)
     return dc::fail(DC_EINVAL, "dc_plan_decode_fill: bad arguments");
-  int32_t top = 1;
+  int32_t top = 0;
   for (int32_t b = 0; b < n_seqs; ++b) {
     if (seq_pages[b] <= 0)
       return dc::fail(DC_EINVAL, "decode requires at least one page (sequence %d has %d)", b, seq_pages[b]);
     top = std::max(top, seq_pages[b]);
   }
-  // (1) the smallest pages-per-split (at least min_pages_per_split) whose
-  // near-equal splits fit target_items
-  auto count = [&](int64_t per) {
-    int64_t c = 0;
-    for (int32_t b = 0; b < n_seqs; ++b) c += (seq_pages[b] + per - 1) / per;
-    return c * n_kv_heads;
+  const int64_t cpp = chunks_per_page;
+  if (int64_t(top) * cpp > INT32_MAX) return dc::fail(DC_EINVAL, "dc_plan_decode_fill: sequence too long");
+  if (page_cost && cost_stride < top)
+    return dc::fail(DC_EINVAL, "dc_plan_decode_fill: cost_stride %lld is below the longest sequence's %d pages",
+                    (long long)cost_stride, top);
+  const int32_t S = n_seqs * n_kv_heads;  // streams, s = b * n_kv_heads + h
+  // cost of each stream; without page costs every chunk costs 1
+  std::vector<double> total(S);
+  for (int32_t s = 0; s < S; ++s) {
+    const int32_t pages = seq_pages[s / n_kv_heads];
+    double w = 0.0;
+    if (page_cost) {
+      const float* c = page_cost + int64_t(s) * cost_stride;
+      for (int32_t p = 0; p < pages; ++p) {
+        if (!(c[p] >= 0.f) || !std::isfinite(c[p]))
+          return dc::fail(DC_EINVAL, "dc_plan_decode_fill: page cost %g (stream %d, page %d) is not finite and >= 0",
+                          double(c[p]), s, p);
+        w += c[p];
+      }
+    } else {
+      w = double(pages) * cpp;
+    }
+    total[s] = w;
+  }
+  // (1) splits: one item per stream, then one more split at a time for the
+  // stream with the largest mean item cost total / splits (compared as
+  // products, ties to the longer stream, then the lower index)
+  std::vector<int32_t> splits(S, 1);
+  auto chunks = [&](int32_t s) { return int64_t(seq_pages[s / n_kv_heads]) * cpp; };
+  auto before = [&](int32_t x, int32_t y) {  // true when x's items rank below y's
+    const double lx = total[x] * splits[y], ly = total[y] * splits[x];
+    if (lx != ly) return lx < ly;
+    if (chunks(x) != chunks(y)) return chunks(x) < chunks(y);
+    return x > y;
   };
-  int64_t lo = std::min<int64_t>(min_pages_per_split, top), hi = top;
-  if (count(hi) <= target_items) {
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) / 2;
-      if (count(mid) <= target_items)
-        hi = mid;
-      else
-        lo = mid + 1;
-    }
+  std::vector<int32_t> heap(S);
+  for (int32_t s = 0; s < S; ++s) heap[s] = s;
+  std::make_heap(heap.begin(), heap.end(), before);
+  int64_t used = S;
+  while (used < target_items) {
+    std::pop_heap(heap.begin(), heap.end(), before);
+    const int32_t s = heap.back();
+    if (chunks(s) / (splits[s] + 1) < min_chunks_per_split) break;
+    ++splits[s];
+    ++used;
+    std::push_heap(heap.begin(), heap.end(), before);
   }
-  std::vector<int32_t> splits(n_seqs);
-  int64_t used = 0;
-  for (int32_t b = 0; b < n_seqs; ++b) {
-    splits[b] = int32_t((seq_pages[b] + hi - 1) / hi);
-    used += int64_t(splits[b]) * n_kv_heads;
-  }
-  // (2) the items left in the budget go, one sequence (all its heads) at a
-  // time, to the sequence with the largest items, while its items keep at
-  // least min_pages_per_split pages
-  for (;;) {
-    if (used + n_kv_heads > target_items) break;
-    // largest mean item pages[b] / splits[b] (compared exactly), ties to
-    // the longer sequence
-    int32_t best = -1;
-    for (int32_t b = 0; b < n_seqs; ++b) {
-      if (seq_pages[b] / (splits[b] + 1) < min_pages_per_split) continue;
-      if (best < 0) {
-        best = b;
-        continue;
-      }
-      const int64_t lhs = int64_t(seq_pages[b]) * splits[best], rhs = int64_t(seq_pages[best]) * splits[b];
-      if (lhs > rhs || (lhs == rhs && seq_pages[b] > seq_pages[best])) best = b;
-    }
-    if (best < 0) break;
-    ++splits[best];
-    used += n_kv_heads;
-  }
+  // (2) cuts at whole chunks: without costs split i of n covers
+  // [i len / n, (i + 1) len / n); with costs, cut i is the last chunk
+  // boundary whose cost prefix stays within i / n of the stream's cost
+  // (keeping every item non-empty)
   int32_t ni = 0, nm = 0, np = 0, largest = 0;
-  for (int32_t b = 0; b < n_seqs; ++b) {
-    const int32_t pages = seq_pages[b], sp = splits[b];
-    for (int32_t h = 0; h < n_kv_heads; ++h) {
-      const int32_t first_partial = np;
-      for (int32_t s = 0; s < sp; ++s) {
-        const int32_t pb = int32_t(int64_t(s) * pages / sp), pe = int32_t(int64_t(s + 1) * pages / sp);
-        largest = std::max(largest, pe - pb);
-        if (items && ni < max_items) {
-          dc_work_item& it = items[ni];
-          it.seq = b;
-          it.kv_head = h;
-          it.page_begin = pb;
-          it.page_end = pe;
-          it.partial = sp > 1 ? np : -1;
-          it.reserved[0] = it.reserved[1] = it.reserved[2] = 0;
-        }
-        ++ni;
-        if (sp > 1) ++np;
+  std::vector<double> prefix;
+  std::vector<int64_t> cut;
+  for (int32_t s = 0; s < S; ++s) {
+    const int32_t b = s / n_kv_heads, h = s % n_kv_heads, n = splits[s];
+    const int64_t len = chunks(s);
+    cut.assign(n + 1, 0);
+    cut[n] = len;
+    if (page_cost && total[s] > 0.0 && n > 1) {
+      const float* c = page_cost + int64_t(s) * cost_stride;
+      prefix.assign(len + 1, 0.0);
+      for (int64_t u = 0; u < len; ++u) prefix[u + 1] = prefix[u] + double(c[u / cpp]) / double(cpp);
+      for (int32_t i = 1; i < n; ++i) {
+        const double goal = total[s] * i / n * (1.0 + 1e-12);
+        int64_t u = int64_t(std::upper_bound(prefix.begin(), prefix.end(), goal) - prefix.begin()) - 1;
+        u = std::min<int64_t>(std::max<int64_t>(u, cut[i - 1] + 1), len - (n - i));
+        cut[i] = u;
       }
-      if (sp > 1) {
-        if (merges && nm < max_merges) merges[nm] = dc_merge_item{b, h, first_partial, sp};
-        ++nm;
+    } else {
+      for (int32_t i = 1; i < n; ++i) cut[i] = len * i / n;
+    }
+    const int32_t first_partial = np;
+    for (int32_t i = 0; i < n; ++i) {
+      const int64_t u0 = cut[i], u1 = cut[i + 1];
+      largest = std::max<int32_t>(largest, int32_t(u1 - u0));
+      if (items && ni < max_items) {
+        dc_work_item& it = items[ni];
+        it.seq = b;
+        it.kv_head = h;
+        it.page_begin = int32_t(u0 / cpp);
+        it.chunk_begin = int32_t(u0 % cpp);
+        it.page_end = int32_t((u1 + cpp - 1) / cpp);
+        it.chunk_end = int32_t(u1 % cpp);
+        it.partial = n > 1 ? np : -1;
+        it.reserved = 0;
       }
+      ++ni;
+      if (n > 1) ++np;
+    }
+    if (n > 1) {
+      if (merges && nm < max_merges) merges[nm] = dc_merge_item{b, h, first_partial, n};
+      ++nm;
     }
   }
   *n_items = ni;

@@ -33,7 +33,8 @@ struct DecodeArgs {
 // shapes is skipped, not read: a fault guard only (hosts validate plans).
 __device__ __forceinline__ bool item_in_bounds(const dc_work_item& it, const DecodeArgs& a) {
   return it.seq >= 0 && it.seq < a.n_seqs && it.kv_head >= 0 && it.kv_head < a.n_kv_heads && it.page_begin >= 0 &&
-         it.page_begin <= it.page_end && it.page_end <= a.table_stride;
+         it.page_begin <= it.page_end && it.page_end <= a.table_stride && it.chunk_begin >= 0 &&
+         it.chunk_begin < (1 << 16) && it.chunk_end >= 0 && it.chunk_end < (1 << 16);
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -102,22 +102,27 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
     if ((int64_t(vd.block) << 8) + VL.total > a.vpool.arena_bytes) continue;
     int32_t T = kd.tokens < vd.tokens ? kd.tokens : vd.tokens;
     if (T > geo.page_capacity) T = geo.page_capacity;
-    if (T <= 0) continue;
+    // the item's tokens of this page, [tl, tl + Tn): it may start and end
+    // inside a page, on 32-token chunk boundaries
+    const int32_t tl = p == it.page_begin ? 32 * it.chunk_begin : 0;
+    const int32_t th = p == it.page_end - 1 && it.chunk_end > 0 ? min(T, 32 * it.chunk_end) : T;
+    const int32_t Tn = th - tl;
+    if (Tn <= 0) continue;
     const uint8_t* kb = blob_ptr(a.kpool.arena, kd);
     const uint8_t* vb = blob_ptr(a.vpool.arena, vd);
 
     // ---- score: thread (token, part); parts split the channels ----
-    for (int32_t t0 = 0; t0 < T; t0 += kTokChunk) {
+    for (int32_t t0 = 0; t0 < Tn; t0 += kTokChunk) {
       const int32_t t = t0 + (tid % kTokChunk), part = tid / kTokChunk;
       float s[kMaxQ];
 #pragma unroll
       for (int j = 0; j < kMaxQ; ++j) s[j] = 0.f;
-      if (t < T) {
+      if (t < Tn) {
         if (is_m0(kd.format)) {
-          score_partial_m0(kb, kd, KL, geo, t, part, qs, qsum, phd, nq, s);
+          score_partial_m0(kb, kd, KL, geo, t + tl, part, qs, qsum, phd, nq, s);
         } else {
           for (int32_t c = part; c < hd; c += kParts) {
-            const float v = page_value(kb, kd, KL, geo, t, c);
+            const float v = page_value(kb, kd, KL, geo, t + tl, c);
 #pragma unroll
             for (int j = 0; j < kMaxQ; ++j)
               if (j < nq) s[j] += v * qs[j * phd + c];
@@ -129,7 +134,7 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
       __syncthreads();
       for (int32_t i = tid; i < nq * kTokChunk; i += kThreads) {
         const int32_t j = i / kTokChunk, tt = i - j * kTokChunk;
-        if (t0 + tt < T) prob[j][t0 + tt] = (red[0][j][tt] + red[1][j][tt] + red[2][j][tt] + red[3][j][tt]) * kLog2e;
+        if (t0 + tt < Tn) prob[j][t0 + tt] = (red[0][j][tt] + red[1][j][tt] + red[2][j][tt] + red[3][j][tt]) * kLog2e;
       }
       __syncthreads();
     }
@@ -138,12 +143,12 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
     const int32_t wave = tid / 64, lane = tid % 64;
     for (int32_t j = wave; j < nq; j += kThreads / 64) {
       float mx = -INFINITY;
-      for (int32_t t = lane; t < T; t += 64) mx = fmaxf(mx, prob[j][t]);
+      for (int32_t t = lane; t < Tn; t += 64) mx = fmaxf(mx, prob[j][t]);
       mx = wave_max(mx);
       const float m_old = m_run[j];
       const float m_new = fmaxf(m_old, mx);
       float sum = 0.f;
-      for (int32_t t = lane; t < T; t += 64) {
+      for (int32_t t = lane; t < Tn; t += 64) {
         const float e = exp2f(prob[j][t] - m_new);
         prob[j][t] = e;
         sum += e;
@@ -163,8 +168,8 @@ __global__ void __launch_bounds__(kThreads) decode_generic_kernel(DecodeArgs a) 
       const int32_t c = tid;
 #pragma unroll
       for (int j = 0; j < kMaxQ; ++j) acc[j] *= alpha[j];
-      for (int32_t t = 0; t < T; ++t) {
-        const float v = page_value(vb, vd, VL, vgeo, t, c);
+      for (int32_t t = 0; t < Tn; ++t) {
+        const float v = page_value(vb, vd, VL, vgeo, t + tl, c);
 #pragma unroll
         for (int j = 0; j < kMaxQ; ++j)
           if (j < nq) acc[j] += prob[j][t] * v;

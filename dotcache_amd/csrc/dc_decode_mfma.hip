@@ -1038,27 +1038,36 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     if (bad) T = 0;
     const uint32_t info = uint32_t(T) | (uint32_t(kf) << 16) | (uint32_t(vf) << 24);
     const uint32_t koffs = ksc | (kbs << 16), voffs = vsc | (vbs << 16);  // offsets < 64 KiB for M0 pages
-    const int nch = (T + 31) >> 5;  // < 16 (capacity <= 256)
-    // end chunk of page lane (inclusive prefix sum over the lanes).  Every
-    // page of the batch full, with a power-of-two count of chunks per page
-    // (2^cps): page lane ends at chunk (lane + 1) 2^cps and chunk j lies in
-    // page j >> cps.  Otherwise bit by bit: ballot of the bit, count of set
-    // lanes at or below this one.
+    const int nch = (T + 31) >> 5;  // <= 8 (capacity <= 256)
+    // The item's chunks of page lane: [lo, hi).  It starts at chunk cb of
+    // its first page (lane 0 of the first batch: `off` chunks skipped) and,
+    // with ce > 0, ends after chunk ce - 1 of its last page.
     const int cpp = CAP >> 5, cps = __builtin_ctz(uint32_t(cpp));
+    const int cb = min(it.chunk_begin, cpp - 1), ce = min(it.chunk_end, cpp);
+    const int off = base == 0 ? cb : 0;
+    const bool last_batch = base + nb == np;
+    const int lo = lane == 0 ? off : 0;
+    const int hi = last_batch && ce > 0 && lane == nb - 1 ? min(nch, ce) : nch;
+    const int cnt = max(hi - lo, 0);
+    // Every page of the batch full, with a power-of-two count of chunks per
+    // page (2^cps): the batch's chunk j is chunk g = j + off of the pages
+    // laid end to end, in page g >> cps.  Otherwise an inclusive prefix sum
+    // of cnt over the lanes, bit by bit (ballot of the bit, count of set
+    // lanes at or below this one): page lane holds chunks [cend - cnt, cend).
     const bool fast = __ballot(lane < nb && T != CAP) == 0 && (cpp & (cpp - 1)) == 0;
     int cend = 0;
-    if (fast) {
-      cend = (lane < nb ? lane + 1 : nb) << cps;
-    } else {
+    if (!fast) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int bit = (nch >> b) & 1;
+        const int bit = (cnt >> b) & 1;
         const uint64_t bal = __ballot(bit);
         const int below = __builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u));
         cend += (below + bit) << b;
       }
     }
-    const int total = fast ? nb << cps : __builtin_amdgcn_readlane(cend, 63);
+    const int cbeg = cend - cnt;
+    const int total = fast ? max((nb << cps) - off - (last_batch && ce > 0 ? cpp - ce : 0), 0)
+                           : __builtin_amdgcn_readlane(cend, 63);
     if (total == 0) continue;
     // chunk j lies in the first page whose end chunk exceeds j
     // a chunk past the end: the same loads against empty buffer resources,
@@ -1069,7 +1078,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       return m;
     };
     auto chunk_meta = [&](int j) __attribute__((always_inline)) -> PageMeta {
-      const int i = fast ? j >> cps : __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
+      const int i = fast ? (j + off) >> cps : __builtin_amdgcn_readfirstlane(int(__popcll(__ballot(cend <= j))));
       PageMeta m;
       // blob pointers stay derived from the arena arguments (global memory)
       const uint8_t* kp =
@@ -1088,7 +1097,7 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
       m.kbs = ko >> 16;
       m.vsc = vo & 0xffff;
       m.vbs = vo >> 16;
-      m.c0 = fast ? (j & (cpp - 1)) * 32 : (j - (__builtin_amdgcn_readlane(cend, i) - ((m.T + 31) >> 5))) * 32;
+      m.c0 = fast ? ((j + off) & (cpp - 1)) * 32 : (j - __builtin_amdgcn_readlane(cbeg, i) + (i == 0 ? off : 0)) * 32;
       return m;
     };
 

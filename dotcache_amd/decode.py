@@ -4,11 +4,13 @@ A decode call covers a batch of sequences x KV heads of one layer.  Page
 tables are int32 ``[n_seqs, n_kv_heads, table_stride]`` arrays of page ids in
 one :class:`~dotcache_amd.page_pool.DevicePagePool`; sequences may have
 different page counts (ragged batch) and their pages may sit anywhere in the
-arena.  The host planner (``dc_plan_decode``) splits long page lists into
-work items of ``pages_per_split`` pages (split-K); the kernel writes
+arena.  The host planner splits long page lists into work items (split-K):
+``dc_plan_decode`` into items of ``pages_per_split`` pages,
+``dc_plan_decode_fill`` into a launch's budget of items of near-equal cost,
+cut on 32-token chunk boundaries inside pages.  The kernel writes
 ``(m, l, o)`` partials for split items and the merge pass combines them by
-log-sum-exp.  Plans are cached per (page counts, heads, split) so a steady
-decode loop uploads nothing.
+log-sum-exp.  Plans are cached per (page counts, heads, split, costs) so a
+steady decode loop uploads nothing.
 """
 from __future__ import annotations
 
@@ -27,6 +29,12 @@ from .page_pool import DevicePagePool, current_stream_ptr, dtype_code
 # split-K partials a small fraction of the bytes read.
 DEFAULT_TARGET_ITEMS = 1024
 MIN_PAGES_PER_SPLIT = 2
+# Planner cost of a page (page_costs): its compressed key and value bytes
+# plus this much per 32-token chunk.  Measured on MI355X with one wave per
+# SIMD, a 32-token chunk of 4-bit M0 keys and values at head_dim 256 (10 KiB)
+# took a wave 2.4 us and one of fp16 keys and values (32 KiB) 5.4 us: about
+# 1.0 us plus 7.5 GB/s per wave, and 1.0 us is worth about 8 KiB at that rate.
+CHUNK_COST_BYTES = 8192
 
 
 def _torch():
@@ -42,21 +50,24 @@ class DecodePlan:
     n_items: int
     n_merges: int
     n_partials: int
-    pages_per_split: int
+    pages_per_split: int              # largest item, in (whole or partly covered) pages
     host_items: np.ndarray            # int32 [n_items, 8]: dc_work_item fields
     host_merges: np.ndarray | None = None  # int32 [n_merges, 4]: dc_merge_item fields
     checked: set = None               # (seq_pages, n_kv_heads, table_stride) keys already validated
+    chunks_per_page: int = 1          # the page split granularity the items were cut for
+    largest_chunks: int = 0           # largest item in 32-token chunks (fill plans)
 
-    def check(self, seq_pages: np.ndarray, n_kv_heads: int, table_stride: int) -> None:
+    def check(self, seq_pages: np.ndarray, n_kv_heads: int, table_stride: int, chunks_per_page: int = 1) -> None:
         """Raise ValueError unless every work item and merge item of the plan
         stays inside these shapes: sequence < n_seqs, KV head < n_kv_heads,
         pages within the sequence's count (and so within the page table),
-        partial slots below n_partials, and device buffers as long as the
-        counts.  The kernels read items without checking them against the
-        tables, so a plan built for other shapes must not reach them.
-        Validated once per shape key."""
+        chunk offsets within a page of ``chunks_per_page`` chunks (and cut
+        for that many), partial slots below n_partials, and device buffers
+        as long as the counts.  The kernels read items without checking them
+        against the tables, so a plan built for other shapes must not reach
+        them.  Validated once per shape key."""
         sp = np.asarray(seq_pages, dtype=np.int64)
-        key = (sp.tobytes(), int(n_kv_heads), int(table_stride))
+        key = (sp.tobytes(), int(n_kv_heads), int(table_stride), int(chunks_per_page))
         if self.checked is None:
             self.checked = set()
         if key in self.checked:
@@ -73,6 +84,14 @@ class DecodePlan:
             raise ValueError("plan: a work item's pages lie outside its sequence's page table")
         if np.any(part >= self.n_partials):
             raise ValueError("plan: a work item names a partial slot past n_partials")
+        cb, ce = it[:, 5], it[:, 6]
+        if np.any(cb != 0) or np.any(ce != 0):
+            if int(self.chunks_per_page) != int(chunks_per_page):
+                raise ValueError(f"plan: items cut for {self.chunks_per_page} chunks per page, pool pages hold "
+                                 f"{chunks_per_page}")
+            if (np.any((cb < 0) | (cb >= chunks_per_page)) or np.any((ce < 0) | (ce > chunks_per_page))
+                    or np.any((pe - pb == 1) & (ce > 0) & (ce <= cb))):
+                raise ValueError("plan: a work item's chunk range lies outside its pages")
         if self.n_merges:
             m = np.asarray(self.host_merges, dtype=np.int64).reshape(-1, 4)
             if m.shape[0] != self.n_merges or self.merges is None or self.merges.numel() < 16 * self.n_merges:
@@ -122,13 +141,54 @@ def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items:
     return int(lo)
 
 
+def chunks_per_page(page_capacity: int) -> int:
+    """32-token chunks in a page of this capacity: the finest split a plan
+    may cut pages at."""
+    return max(1, (int(page_capacity) + 31) // 32)
+
+
+def page_costs(k_pool: DevicePagePool, v_pool: DevicePagePool, k_table, v_table, seq_pages) -> np.ndarray:
+    """float32 ``[n_seqs, n_kv_heads, table_stride]``: each page's decode
+    cost for :func:`make_plan`, 0 past a sequence's pages.  ``k_table`` /
+    ``v_table``: host int32 page ids.
+
+    Within a stream (one sequence and KV head) a page costs its key and
+    value bytes of valid tokens plus ``CHUNK_COST_BYTES`` per started
+    32-token chunk, so the item holding an exact recent window gets fewer
+    pages.  Each stream's costs are then scaled to sum to its page count:
+    between streams the planner balances page counts.  Measured on MI355X,
+    a batch whose exact (fp16) key streams got smaller items by their byte
+    cost ran slower (C4 shape: 51.5 against 50.7 us per layer): the exact
+    streams' waves share HBM with the others, so their items run no longer
+    than the rest when all are the same size."""
+    kt = np.asarray(k_table, dtype=np.int64)
+    vt = np.asarray(v_table, dtype=np.int64)
+    if kt.ndim != 3 or vt.shape != kt.shape:
+        raise ValueError("page tables must have shape [n_seqs, n_kv_heads, table_stride]")
+    sp = np.asarray(seq_pages, dtype=np.int64)
+    live = np.arange(kt.shape[2])[None, None, :] < sp[:, None, None]
+    kt = np.where(live, kt, 0)
+    vt = np.where(live, vt, 0)
+    tok = k_pool.tokens_of(kt)
+    raw = k_pool.read_bytes_each(kt) + v_pool.read_bytes_each(vt) + CHUNK_COST_BYTES * ((tok + 31) // 32)
+    raw = np.where(live, raw, 0).astype(np.float64)
+    total = raw.sum(axis=2, keepdims=True)
+    scale = np.where(total > 0, sp[:, None, None] / np.maximum(total, 1.0), 0.0)
+    cost = np.where(total > 0, raw * scale, live.astype(np.float64))
+    return cost.astype(np.float32)
+
+
 def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *, device="cuda",
-              target_items: int | None = None) -> DecodePlan:
+              target_items: int | None = None, chunks_per_page: int = 1, page_cost=None) -> DecodePlan:
     """Work and merge items for a batch with these page counts.  With
-    ``pages_per_split`` the near-equal splits of ``dc_plan_decode``; without
-    it ``dc_plan_decode_fill``: the smallest such split that fits
-    ``target_items`` (default: one item per SIMD), then the rest of that
-    budget spent on further splits of the sequences with the largest items.
+    ``pages_per_split`` the near-equal splits of ``dc_plan_decode`` (whole
+    pages).  Without it ``dc_plan_decode_fill``: ``target_items`` (default:
+    one per SIMD) items of near-equal cost, cut at 32-token chunk
+    boundaries when ``chunks_per_page`` > 1 (pass
+    :func:`chunks_per_page` of the pool's page capacity), with each page
+    costing ``page_cost[b, h, page]`` (float ``[n_seqs, n_kv_heads, >= max
+    pages]``; default: the same for every chunk).  No item has fewer than
+    ``MIN_PAGES_PER_SPLIT`` pages' worth of chunks unless its stream does.
     ``DecodePlan.pages_per_split`` is the largest item's page count."""
     torch = _torch()
     sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
@@ -139,7 +199,16 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     fill = pages_per_split is None
     pps = 0 if fill else int(pages_per_split)
     target = (int(target_items) if target_items else default_target_items()) if fill else 0
-    key = (sp.tobytes(), int(n_kv_heads), pps, target, str(device))
+    cpp = int(chunks_per_page) if fill else 1
+    if cpp <= 0:
+        raise ValueError("chunks_per_page must be positive")
+    cost = None
+    if fill and page_cost is not None:
+        cost = np.ascontiguousarray(np.asarray(page_cost, dtype=np.float32))
+        if cost.ndim != 3 or cost.shape[:2] != (sp.size, int(n_kv_heads)) or cost.shape[2] < int(sp.max()):
+            raise ValueError("page_cost must have shape [n_seqs, n_kv_heads, >= max pages]")
+    key = (sp.tobytes(), int(n_kv_heads), pps, target, cpp, None if cost is None else (cost.shape, cost.tobytes()),
+           str(device))
     hit = _plan_cache.get(key)
     if hit is not None:
         return hit
@@ -148,9 +217,11 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
 
     def plan(items_p, max_items, merges_p, max_merges):
         if fill:
-            return L.dc_plan_decode_fill(sp.ctypes.data, sp.size, n_kv_heads, target, MIN_PAGES_PER_SPLIT, items_p,
-                                         max_items, C.byref(ni), merges_p, max_merges, C.byref(nm), C.byref(npart),
-                                         C.byref(big))
+            return L.dc_plan_decode_fill(sp.ctypes.data, sp.size, n_kv_heads, cpp,
+                                         None if cost is None else cost.ctypes.data,
+                                         0 if cost is None else cost.shape[2], target, MIN_PAGES_PER_SPLIT * cpp,
+                                         items_p, max_items, C.byref(ni), merges_p, max_merges, C.byref(nm),
+                                         C.byref(npart), C.byref(big))
         return L.dc_plan_decode(sp.ctypes.data, sp.size, n_kv_heads, pps, items_p, max_items, C.byref(ni), merges_p,
                                 max_merges, C.byref(nm), C.byref(npart))
 
@@ -162,12 +233,13 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     st = plan(C.addressof(items), ni.value, C.addressof(merges), nm.value)
     _lib.check(st, "dc_plan_decode")
     if fill:
-        pps = int(big.value)
+        pps = -(-int(big.value) // cpp)
     host_items = np.frombuffer(bytes(items), dtype=np.int32).reshape(-1, 8)[: ni.value].copy()
     host_merges = np.frombuffer(bytes(merges), dtype=np.int32).reshape(-1, 4)[: nm.value].copy()
     dev_items = torch.frombuffer(bytearray(bytes(items)), dtype=torch.uint8).to(device)
     dev_merges = torch.frombuffer(bytearray(bytes(merges)), dtype=torch.uint8).to(device) if nm.value else None
-    plan = DecodePlan(dev_items, dev_merges, ni.value, nm.value, npart.value, pps, host_items, host_merges)
+    plan = DecodePlan(dev_items, dev_merges, ni.value, nm.value, npart.value, pps, host_items, host_merges,
+                      chunks_per_page=cpp, largest_chunks=int(big.value) if fill else pps)
     if len(_plan_cache) > 256:
         _plan_cache.clear()
     _plan_cache[key] = plan
@@ -257,9 +329,10 @@ def decode_paged(
             vpool.validate_ids(ids_v)
             if not np.array_equal(pool.tokens_of(ids_k), vpool.tokens_of(ids_v)):
                 raise ValueError("key and value pages must hold the same token counts")
+    cpp = chunks_per_page(pool.geometry.page_capacity)
     if plan is None:
-        plan = make_plan(sp, H, pages_per_split, device=queries.device)
-    plan.check(sp, H, stride)
+        plan = make_plan(sp, H, pages_per_split, device=queries.device, chunks_per_page=cpp)
+    plan.check(sp, H, stride, cpp)
     if not queries.is_contiguous():
         queries = queries.contiguous()
     if out is None:

@@ -430,9 +430,18 @@ class DevicePagePool:
 
     def read_bytes(self, page_ids) -> int:
         """Compressed bytes a reader fetches for these pages (valid tokens only)."""
-        total = 0
+        return int(self.read_bytes_each(page_ids).sum())
+
+    def read_bytes_each(self, page_ids) -> np.ndarray:
+        """int64 array shaped like ``page_ids``: each page's compressed bytes
+        a reader fetches (valid tokens only)."""
+        ids = np.asarray(page_ids, dtype=np.int64)
+        if ids.size == 0:
+            return np.zeros(ids.shape, dtype=np.int64)
+        d = self._host_desc[ids.ravel()]
+        key = (d["format"].astype(np.int64) << 32) | (d["bits"].astype(np.int64) << 16) | d["tokens"].astype(np.int64)
+        uniq, inv = np.unique(key, return_inverse=True)
         geo = self.geometry.c()
-        for pid in np.asarray(page_ids, dtype=np.int64).ravel():
-            d = self._host_desc[pid]
-            total += _lib.page_read_bytes(int(d["format"]), int(d["bits"]), int(d["tokens"]), geo)
-        return total
+        each = np.array([_lib.page_read_bytes(int(u >> 32), int((u >> 16) & 0xFFFF), int(u & 0xFFFF), geo)
+                         for u in uniq], dtype=np.int64)
+        return each[inv.ravel()].reshape(ids.shape)

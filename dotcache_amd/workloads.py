@@ -14,7 +14,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib
-from .decode import DecodePlan, decode_paged, make_plan, merge_partials, workspace_bytes
+from .decode import DecodePlan, chunks_per_page, decode_paged, make_plan, merge_partials, page_costs, workspace_bytes
 from .page_pool import DevicePagePool, PoolGeometry
 
 
@@ -124,7 +124,8 @@ class Workload:
     queries: list              # per layer [B, H, Q, hd] bf16
     new_k: list = field(default_factory=list)  # per layer [B*H, hd] rows to append
     new_v: list = field(default_factory=list)
-    plan: DecodePlan | None = None
+    plan: DecodePlan | None = None  # layer 0's plan (every layer's when a split is given)
+    plans: list = field(default_factory=list)  # per layer: items of near-equal cost under its page formats
     outs: list = field(default_factory=list)
     workspace: object = None
     k_page_ids_by_layer: list = field(default_factory=list)
@@ -193,14 +194,14 @@ class Workload:
         self.decode_kernel(l)
 
     def merge_kernel(self, l: int) -> None:
-        merge_partials(self.plan, self.outs[l], self.workspace)
+        merge_partials(self.plans[l], self.outs[l], self.workspace)
 
     def decode_kernel(self, l: int) -> None:
         """Layer ``l``'s decode kernel alone (``dc_decode_paged`` without
         the merge)."""
         lt = self.layers[l]
         decode_paged(self.k_pool, lt.k_table, lt.v_table, lt.seq_pages, self.queries[l],
-                     query_scale=self.query_scale, plan=self.plan, out=self.outs[l], workspace=self.workspace,
+                     query_scale=self.query_scale, plan=self.plans[l], out=self.outs[l], workspace=self.workspace,
                      validate=False, v_pool=self.v_pool, merge=False)
 
     def capture(self) -> None:
@@ -304,6 +305,7 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
     tables: list[LayerTables] = []
     queries, new_k, new_v = [], [], []
     kids_by_layer, vids_by_layer = [], []
+    kids_tables, vids_tables = [], []
     attended = lengths.copy()
     for l in range(n_sets):
         gen.manual_seed(seed * 1000 + l)
@@ -377,6 +379,8 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
         tables.append(lt)
         kt_now = lt.k_table.cpu().numpy()
         vt_now = lt.v_table.cpu().numpy()
+        kids_tables.append(kt_now)
+        vids_tables.append(vt_now)
         kids_by_layer.append(np.concatenate([kt_now[b, :, : lt.seq_pages[b]].ravel() for b in range(B)]))
         vids_by_layer.append(np.concatenate([vt_now[b, :, : lt.seq_pages[b]].ravel() for b in range(B)]))
         queries.append((torch.randn((B, H, Q, hd), generator=gen, device=dev)).to(torch.bfloat16))
@@ -385,8 +389,18 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
     wl = Workload(spec=spec, seed=seed, lengths=lengths, k_pool=k_pool, v_pool=v_pool, layers=tables, queries=queries,
                   new_k=new_k, new_v=new_v, k_page_ids_by_layer=kids_by_layer, v_page_ids_by_layer=vids_by_layer,
                   attended=attended)
-    wl.plan = make_plan(tables[0].seq_pages, H, pages_per_split, device=dev)
-    wl.workspace = torch.zeros(max(workspace_bytes(wl.plan, Q, hd), 16), dtype=torch.uint8, device=dev)
+    # per layer: a launch's budget of items cut at 32-token chunks, each
+    # stream cut by its pages' costs (an exact recent window reads more
+    # bytes per token)
+    cpp = chunks_per_page(P)
+    for l, lt in enumerate(tables):
+        cost = None
+        if pages_per_split is None:
+            cost = page_costs(k_pool, v_pool, kids_tables[l], vids_tables[l], lt.seq_pages)
+        wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp, page_cost=cost))
+    wl.plan = wl.plans[0]
+    need = max(workspace_bytes(p, Q, hd) for p in wl.plans)
+    wl.workspace = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)
     wl.outs = [torch.empty((B, H, Q, hd), dtype=torch.float32, device=dev) for _ in range(n_sets)]
     if spec.append:
         wl.tail_k_dev = [torch.from_numpy(t.tail_k.ravel().astype(np.int32)).to(dev) for t in tables]

@@ -97,14 +97,22 @@ typedef struct dc_pool {
 /* One unit of decode work: pages [page_begin, page_end) of one
  * (sequence, kv_head).  partial < 0: the item covers the whole sequence and
  * writes the normalised output; otherwise it writes split-K partial
- * (m, l, o) slot `partial`. */
+ * (m, l, o) slot `partial`.  An item may start and end inside a page, on
+ * 32-token chunk boundaries: it skips the first chunk_begin chunks of page
+ * page_begin and, when chunk_end > 0, stops after chunk chunk_end - 1 of
+ * page page_end - 1 (with one page, chunks [chunk_begin, chunk_end) of it).
+ * Both 0 (as dc_plan_decode writes them) cover whole pages.  Valid values:
+ * 0 <= chunk_begin < ceil(page_capacity / 32), 0 <= chunk_end <=
+ * ceil(page_capacity / 32). */
 typedef struct dc_work_item {
   int32_t seq;
   int32_t kv_head;
   int32_t page_begin;
   int32_t page_end;
   int32_t partial;
-  int32_t reserved[3];
+  int32_t chunk_begin;
+  int32_t chunk_end;
+  int32_t reserved;
 } dc_work_item;
 
 /* Log-sum-exp merge of partials [partial_begin, partial_begin + count) into
@@ -256,18 +264,27 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
                    dc_work_item* items, int32_t max_items, int32_t* n_items,
                    dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials);
 
-/* Host-only planner that fills a launch: the near-equal splits of
- * dc_plan_decode with the smallest pages-per-split (at least
- * min_pages_per_split) that keeps n_kv_heads x sum(splits) <= target_items,
- * then, while the budget allows, one more split (for all heads) of the
- * sequence whose items are largest, as long as its items keep at least
- * min_pages_per_split pages.  target_items is normally one item per SIMD.
- * Same items, merges and DC_ESPACE convention as dc_plan_decode; *largest_item
- * receives the largest item's page count.  The chunking of the reference's
- * grouped decode (dotcache/backends/torch_mps.py:4110-4273) has no launch
- * to fill; this planner has no reference counterpart beyond it. */
-int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t target_items,
-                        int32_t min_pages_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
+/* Host-only planner that fills a launch with items of near-equal cost.
+ * Each (sequence, kv_head) stream is a run of seq_pages[b] x chunks_per_page
+ * chunks (32 tokens each; chunks_per_page = ceil(page_capacity / 32) lets
+ * items split pages, 1 keeps them whole).  A chunk costs page_cost[(b *
+ * n_kv_heads + h) * cost_stride + page] / chunks_per_page, or 1 when
+ * page_cost is NULL (costs must be finite and >= 0).  Starting from one item
+ * per stream, the planner adds one split at a time to the stream with the
+ * largest mean item cost (ties to the longer stream, then the lower index)
+ * while fewer than target_items items exist and that stream's items keep at
+ * least min_chunks_per_split chunks; it stops at the first stream that
+ * cannot be split further, whose items then bound the launch.  Each stream
+ * is then cut at its cost quantiles (whole-chunk boundaries; without costs,
+ * split s of n covers chunks [s·len/n, (s+1)·len/n)).  target_items is
+ * normally one item per SIMD.  Same items, merges and DC_ESPACE convention
+ * as dc_plan_decode; *largest_item receives the largest item's chunk count.
+ * The chunking of the reference's grouped decode
+ * (dotcache/backends/torch_mps.py:4110-4273) has no launch to fill; this
+ * planner has no reference counterpart beyond it. */
+int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t chunks_per_page,
+                        const float* page_cost, int64_t cost_stride, int32_t target_items,
+                        int32_t min_chunks_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
                         dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials,
                         int32_t* largest_item);
 

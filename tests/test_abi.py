@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().dc_abi_version() == 1
+    assert _lib.lib().dc_abi_version() == 2
 
 
 def test_blob_bytes_match_layout():
@@ -77,33 +77,48 @@ def test_planner_covers_every_page_once():
     assert sorted(ms) == [(0, 0, 0, 2), (0, 1, 2, 2), (2, 0, 4, 3), (2, 1, 7, 3)]
 
 
-def _plan_fill(seq_pages, heads, target, min_pages=2):
+def _plan_fill(seq_pages, heads, target, cpp=1, cost=None, min_chunks=None):
+    """dc_plan_decode_fill; items as (seq, head, first chunk, end chunk,
+    partial) with chunk positions counted along the stream."""
     sp = np.asarray(seq_pages, dtype=np.int32)
     L = _lib.lib()
+    min_chunks = 2 * cpp if min_chunks is None else min_chunks
+    cp, stride = None, 0
+    if cost is not None:
+        cost = np.ascontiguousarray(cost, dtype=np.float32)
+        cp, stride = cost.ctypes.data, cost.shape[2]
     ni, nm, npart, big = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
-    st = L.dc_plan_decode_fill(sp.ctypes.data, sp.size, heads, target, min_pages, None, 0, C.byref(ni), None, 0,
-                               C.byref(nm), C.byref(npart), C.byref(big))
+    args = (sp.ctypes.data, sp.size, heads, cpp, cp, stride, target, min_chunks)
+    st = L.dc_plan_decode_fill(*args, None, 0, C.byref(ni), None, 0, C.byref(nm), C.byref(npart), C.byref(big))
     if st != _lib.DC_ESPACE:
         _lib.check(st, "plan fill")
     items = (_lib.WorkItem * max(ni.value, 1))()
     merges = (_lib.MergeItem * max(nm.value, 1))()
-    st = L.dc_plan_decode_fill(sp.ctypes.data, sp.size, heads, target, min_pages, C.addressof(items), ni.value,
-                               C.byref(ni), C.addressof(merges), nm.value, C.byref(nm), C.byref(npart), C.byref(big))
+    st = L.dc_plan_decode_fill(*args, C.addressof(items), ni.value, C.byref(ni), C.addressof(merges), nm.value,
+                               C.byref(nm), C.byref(npart), C.byref(big))
     _lib.check(st, "plan fill")
-    its = [(i.seq, i.kv_head, i.page_begin, i.page_end, i.partial) for i in items[: ni.value]]
+    its = []
+    for i in items[: ni.value]:
+        assert 0 <= i.chunk_begin < cpp and 0 <= i.chunk_end < cpp and i.reserved == 0
+        u0 = i.page_begin * cpp + i.chunk_begin
+        u1 = i.page_end * cpp if i.chunk_end == 0 else (i.page_end - 1) * cpp + i.chunk_end
+        its.append((i.seq, i.kv_head, u0, u1, i.partial))
     ms = [(m.seq, m.kv_head, m.partial_begin, m.count) for m in merges[: nm.value]]
     return its, ms, npart.value, big.value
 
 
-def _check_plan_shape(its, ms, npart, seq_pages, heads):
-    """Every (sequence, head) covers its pages once, in order, by near-equal
-    items; split streams own consecutive partial slots named by their merge."""
+def _check_plan_shape(its, ms, npart, seq_pages, heads, cpp=1, equal=True):
+    """Every (sequence, head) covers its chunks once, in order, by non-empty
+    (without costs: near-equal) items; split streams own consecutive partial
+    slots named by their merge."""
     for b, n in enumerate(seq_pages):
         for h in range(heads):
-            mine = [(pb, pe, part) for (s, hh, pb, pe, part) in its if s == b and hh == h]
-            assert [p for (pb, pe, _) in mine for p in range(pb, pe)] == list(range(n))
-            sizes = [pe - pb for (pb, pe, _) in mine]
-            assert max(sizes) - min(sizes) <= 1
+            mine = [(u0, u1, part) for (s, hh, u0, u1, part) in its if s == b and hh == h]
+            assert [u for (u0, u1, _) in mine for u in range(u0, u1)] == list(range(n * cpp))
+            sizes = [u1 - u0 for (u0, u1, _) in mine]
+            assert min(sizes) >= 1
+            if equal:
+                assert max(sizes) - min(sizes) <= 1
             if len(mine) == 1:
                 assert mine[0][2] == -1
             else:
@@ -113,29 +128,73 @@ def _check_plan_shape(its, ms, npart, seq_pages, heads):
 
 
 def test_fill_planner_uses_the_whole_budget():
-    """C5's shape (4 x 4 streams of 1025 pages, one item per SIMD): the
-    page-count split leaves 976 items (17 pages); the fill planner spends the
-    other 48 on three more splits per stream, 64 items of 16 or 17 pages."""
+    """C5's shape (4 x 4 streams of 1025 pages, one item per SIMD): whole
+    pages give 64 items of 16 or 17 pages per stream; cut at 32-token chunks
+    (4 per 128-token page) the largest item is 65 chunks (16.25 pages)."""
     its, ms, npart, big = _plan_fill([1025] * 4, 4, 1024)
     assert len(its) == 1024 and big == 17 and len(ms) == 16 and all(m[3] == 64 for m in ms)
     _check_plan_shape(its, ms, npart, [1025] * 4, 4)
-    # C3's shape already fills the budget: the plan of dc_plan_decode with 8 pages per split
-    its, ms, npart, big = _plan_fill([256] * 8, 4, 1024)
-    assert len(its) == 1024 and big == 8 and all(pe - pb == 8 for (_, _, pb, pe, _) in its)
+    its, ms, npart, big = _plan_fill([1025] * 4, 4, 1024, cpp=4)
+    assert len(its) == 1024 and big == 65 and all(m[3] == 64 for m in ms)
+    _check_plan_shape(its, ms, npart, [1025] * 4, 4, cpp=4)
+    # C3's shape already fills the budget: 8-page items, which chunk cuts keep on page boundaries
+    for cpp in (1, 2):
+        its, ms, npart, big = _plan_fill([256] * 8, 4, 1024, cpp=cpp)
+        assert len(its) == 1024 and big == 8 * cpp and all(u1 - u0 == 8 * cpp for (_, _, u0, u1, _) in its)
+        assert all(u0 % cpp == 0 for (_, _, u0, _, _) in its)
+
+
+def test_fill_planner_page_costs():
+    """Costed pages: each stream is cut at its cost quantiles, so no item
+    costs more than its stream's mean item cost plus one chunk; the streams
+    with dearer pages get more items."""
+    rng = np.random.default_rng(5)
+    pages = [1025] * 4
+    cost = np.ones((4, 4, 1025), dtype=np.float32)
+    cost[:, :, -2:] = 2.2  # the exact recent window of a long-context pool
+    cost[:, 1, :] *= 1.5    # one KV head's keys held exact
+    cpp = 4
+    its, ms, npart, big = _plan_fill(pages, 4, 1024, cpp=cpp, cost=cost)
+    assert len(its) <= 1024
+    _check_plan_shape(its, ms, npart, pages, 4, cpp=cpp, equal=False)
+    chunk = np.repeat(cost, cpp, axis=2) / cpp
+    per_stream = {}
+    for (b, h, u0, u1, _) in its:
+        per_stream.setdefault((b, h), []).append(float(chunk[b, h, u0:u1].sum()))
+    for (b, h), c in per_stream.items():
+        assert max(c) <= chunk[b, h].sum() / len(c) + chunk[b, h].max() + 1e-6
+    n_items = {k: len(v) for k, v in per_stream.items()}
+    assert all(n_items[(b, 1)] > n_items[(b, 0)] for b in range(4))
+    # the largest item cost is within one chunk of the best split of the budget
+    worst = max(max(c) for c in per_stream.values())
+    assert worst <= chunk.sum() / 1024 * 1.05 + chunk.max()
+    # random costs on ragged streams: same guarantees
+    pages = rng.integers(1, 200, size=12).tolist()
+    cost = rng.uniform(0.5, 3.0, size=(12, 2, 200)).astype(np.float32)
+    its, ms, npart, big = _plan_fill(pages, 2, 150, cpp=2, cost=cost)
+    assert len(its) <= 150
+    _check_plan_shape(its, ms, npart, pages, 2, cpp=2, equal=False)
+    with pytest.raises(ValueError):  # a negative cost
+        bad = cost.copy()
+        bad[0, 0, 0] = -1.0
+        _plan_fill(pages, 2, 150, cpp=2, cost=bad)
+    with pytest.raises(ValueError):  # costs shorter than the longest sequence
+        _plan_fill(pages, 2, 150, cpp=2, cost=cost[:, :, : max(pages) - 1])
 
 
 def test_fill_planner_ragged_and_limits():
     rng = np.random.default_rng(11)
     pages = rng.integers(1, 300, size=20).tolist()
-    its, ms, npart, big = _plan_fill(pages, 2, 100)
-    assert len(its) <= 100
-    _check_plan_shape(its, ms, npart, pages, 2)
-    # no split item below the minimum page count
-    assert all(pe - pb >= 2 for (s, _, pb, pe, part) in its if part >= 0)
-    # never a larger item than the smallest page-count split that fits
-    from dotcache_amd.decode import choose_pages_per_split
+    for cpp in (1, 2, 4):
+        its, ms, npart, big = _plan_fill(pages, 2, 100, cpp=cpp)
+        assert len(its) <= 100
+        _check_plan_shape(its, ms, npart, pages, 2, cpp=cpp)
+        # no split item below the minimum (two pages' chunks)
+        assert all(u1 - u0 >= 2 * cpp for (s, _, u0, u1, part) in its if part >= 0)
+        # never a larger item than the smallest whole-page split that fits
+        from dotcache_amd.decode import choose_pages_per_split
 
-    assert big <= choose_pages_per_split(np.asarray(pages), 2, target_items=100)
+        assert big <= cpp * choose_pages_per_split(np.asarray(pages), 2, target_items=100)
     # more streams than the budget: one item per stream, over the target
     its, ms, npart, big = _plan_fill([3] * 10, 2, 8)
     assert len(its) == 20 and not ms and big == 3
@@ -143,6 +202,28 @@ def test_fill_planner_ragged_and_limits():
         _plan_fill([3, 0], 1, 8)
     with pytest.raises(ValueError):  # no item budget
         _plan_fill([3], 1, 0)
+    with pytest.raises(ValueError):  # no chunks per page
+        _plan_fill([3], 1, 8, cpp=0)
+
+
+def test_make_plan_chunk_fields_and_checks():
+    """make_plan's fill plans carry the chunk cuts; DecodePlan.check rejects
+    them for pools of another page size."""
+    from dotcache_amd.decode import chunks_per_page, make_plan
+
+    assert [chunks_per_page(c) for c in (16, 32, 48, 64, 128, 256)] == [1, 1, 2, 2, 4, 8]
+    plan = make_plan([1025] * 4, 4, device="cpu", target_items=1024, chunks_per_page=4)
+    assert plan.n_items == 1024 and plan.largest_chunks == 65 and plan.pages_per_split == 17
+    cb, ce = plan.host_items[:, 5], plan.host_items[:, 6]
+    assert np.any(cb != 0) and np.any(ce != 0)
+    plan.check(np.full(4, 1025), 4, 1025, 4)
+    with pytest.raises(ValueError):
+        plan.check(np.full(4, 1025), 4, 1025, 2)
+    cost = np.ones((4, 4, 1025), dtype=np.float32)
+    with pytest.raises(ValueError):
+        make_plan([1025] * 4, 4, device="cpu", target_items=1024, chunks_per_page=4, page_cost=cost[:, :2])
+    costed = make_plan([1025] * 4, 4, device="cpu", target_items=1024, chunks_per_page=4, page_cost=cost)
+    assert np.array_equal(costed.host_items, plan.host_items)
 
 
 def test_planner_rejects_empty_sequence():
@@ -198,3 +279,34 @@ def test_mfma_head_block_switch():
             set_mfma_head_block(2)
     finally:
         lib.dc_set_mfma_head_block(0)
+
+
+def test_page_costs_weigh_pages_within_a_stream():
+    """page_costs: within a stream, pages cost their compressed bytes plus a
+    fixed amount per 32-token chunk; each stream's costs sum to its page
+    count; past a sequence's pages the cost is 0."""
+    from dotcache_amd.decode import CHUNK_COST_BYTES, page_costs
+    from dotcache_amd.page_pool import DevicePagePool, PoolGeometry
+
+    geo = PoolGeometry(128, 32, 64)
+    kp = DevicePagePool(geo, device="cpu", reserve_bytes=1 << 20, reserve_pages=32)
+    vp = DevicePagePool(geo, device="cpu", reserve_bytes=1 << 20, reserve_pages=32)
+    m0k = kp.allocate(_lib.FMT_M0_AFFINE, 4, 3, tokens=64)
+    m3k = kp.allocate(_lib.FMT_M3_F16, 0, 2, tokens=64)
+    kp.set_tokens(m3k[1:], 5)  # a partial newest page
+    vids = vp.allocate(_lib.FMT_M0_SYMMETRIC, 4, 5, tokens=64)
+    vp.set_tokens(vids[4:], 5)
+    kt = np.zeros((2, 1, 4), np.int32)
+    vt = np.zeros((2, 1, 4), np.int32)
+    kt[0, 0] = [m0k[0], m0k[1], m0k[2], m3k[0]]  # stream 0: three M0 pages, then an exact page
+    vt[0, 0] = vids[:4]
+    kt[1, 0, :1] = [m3k[1]]                      # stream 1: one partial page
+    vt[1, 0, :1] = [vids[4]]
+    c = page_costs(kp, vp, kt, vt, np.array([4, 1]))
+    g = geo.c()
+    raw = np.array([_lib.page_read_bytes(_lib.FMT_M0_AFFINE, 4, 64, g)] * 3 + [_lib.page_read_bytes(_lib.FMT_M3_F16, 0, 64, g)],
+                   np.float64)
+    raw += _lib.page_read_bytes(_lib.FMT_M0_SYMMETRIC, 4, 64, g) + 2 * CHUNK_COST_BYTES
+    np.testing.assert_allclose(c[0, 0], raw * 4 / raw.sum(), rtol=1e-6)
+    assert c[0, 0, 3] > 1.3 * c[0, 0, 0]  # the exact page reads 16 KiB of keys instead of 5
+    np.testing.assert_allclose(c[1, 0], [1.0, 0.0, 0.0, 0.0])
