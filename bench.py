@@ -66,17 +66,17 @@ def parse():
     return ap.parse_args()
 
 
-def profiled_traffic(workload: str, pages_per_split: int, decode_path: str, head_block: int):
-    """HBM bytes per decode launch measured for this workload by the
-    FETCH_SIZE / WRITE_SIZE runs summarised under profiles/ (calibrated
+def profiled_traffic(workload: str, plan: str, pages_per_split: int, decode_path: str, head_block: int):
+    """HBM bytes per decode launch measured for this workload and plan by
+    the FETCH_SIZE / WRITE_SIZE runs summarised under profiles/ (calibrated
     against a copy of known size there), or None if none matches."""
     import re
 
     for f in sorted((ROOT / "profiles").glob("*.md")):
         for m in re.finditer(r"<!-- traffic (\{.*?\}) -->", f.read_text()):
             rec = json.loads(m.group(1))
-            if (rec.get("workload"), rec.get("pages_per_split"), rec.get("decode_path"), rec.get("head_block")) == (
-                    workload, pages_per_split, decode_path, head_block):
+            if (rec.get("workload"), rec.get("plan"), rec.get("pages_per_split"), rec.get("decode_path"),
+                    rec.get("head_block")) == (workload, plan, pages_per_split, decode_path, head_block):
                 return float(rec["traffic_bytes"])
     return None
 
@@ -305,6 +305,9 @@ def main():
     wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
                         scatter_pages=not args.contiguous_pages, key_bits=args.key_bits)
     spec = wl.spec
+    # "fill": per-layer plans of a launch's item budget cut at 32-token chunks
+    # by page cost; "pages": --pages-per-split whole-page splits
+    plan_kind = "fill" if args.pages_per_split is None else "pages"
     log(f"built in {time.time() - t0:.1f} s: {wl.plan.n_items} work items/layer, pages/split {wl.plan.pages_per_split}, "
         f"K pool {wl.k_pool.arena.numel() / 1e9:.2f} GB, V pool {wl.v_pool.arena.numel() / 1e9:.2f} GB")
 
@@ -438,6 +441,7 @@ def main():
             "key_pages": fmt(spec.key) + (f", {spec.key_m3_fraction:.0%} streams M3" if spec.key_m3_fraction else ""),
             "value_pages": fmt(spec.value),
             "append": spec.append,
+            "plan": plan_kind,
             "pages_per_split": wl.plan.pages_per_split,
             "launch": "eager" if args.eager else "hip graph of the whole step",
             "parallelism": "single GPU",
@@ -452,7 +456,8 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": profiled_traffic(spec.name, wl.plan.pages_per_split, args.decode_path, args.head_block),
+            "traffic": profiled_traffic(spec.name, plan_kind, wl.plan.pages_per_split, args.decode_path,
+                                        args.head_block),
             "kernel": ("decode_generic_kernel" if args.decode_path == "generic" else "decode_mfma_kernel")
                       + " (dc_decode_paged, one launch per layer)",
             "launch_us": launch_ms * 1e3,
