@@ -29,6 +29,12 @@ from .page_pool import DevicePagePool, current_stream_ptr, dtype_code
 # split-K partials a small fraction of the bytes read.
 DEFAULT_TARGET_ITEMS = 1024
 MIN_PAGES_PER_SPLIT = 2
+# The fill planner splits a stream no finer than this many 32-token chunks
+# per item.  Only launches with budget to spare reach it (small batches):
+# on C2 (8 streams of 64 pages) items of 2 chunks took 6.7 us per layer
+# against 8.4 us for 4 chunks (4-page items), with the merge unchanged
+# (4.0 us); single chunks gained nothing more once the merge grew.
+MIN_CHUNKS_PER_SPLIT = 2
 # Planner cost of a page (page_costs): its compressed key and value bytes
 # plus this much per 32-token chunk.  Measured on MI355X with one wave per
 # SIMD, a 32-token chunk of 4-bit M0 keys and values at head_dim 256 (10 KiB)
@@ -188,7 +194,7 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     :func:`chunks_per_page` of the pool's page capacity), with each page
     costing ``page_cost[b, h, page]`` (float ``[n_seqs, n_kv_heads, >= max
     pages]``; default: the same for every chunk).  No item has fewer than
-    ``MIN_PAGES_PER_SPLIT`` pages' worth of chunks unless its stream does.
+    ``MIN_CHUNKS_PER_SPLIT`` chunks unless its stream does.
     ``DecodePlan.pages_per_split`` is the largest item's page count."""
     torch = _torch()
     sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
@@ -219,7 +225,7 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
         if fill:
             return L.dc_plan_decode_fill(sp.ctypes.data, sp.size, n_kv_heads, cpp,
                                          None if cost is None else cost.ctypes.data,
-                                         0 if cost is None else cost.shape[2], target, MIN_PAGES_PER_SPLIT * cpp,
+                                         0 if cost is None else cost.shape[2], target, MIN_CHUNKS_PER_SPLIT,
                                          items_p, max_items, C.byref(ni), merges_p, max_merges, C.byref(nm),
                                          C.byref(npart), C.byref(big))
         return L.dc_plan_decode(sp.ctypes.data, sp.size, n_kv_heads, pps, items_p, max_items, C.byref(ni), merges_p,
