@@ -65,21 +65,27 @@ def test_noalloc_matches_workspace_decode_twice(kfmt, vfmt, hd, Q):
 
     from dotcache_amd import _lib
     from dotcache_amd.backends import clear_prepared_pools
-    from dotcache_amd.decode import decode_paged, make_plan
+    from dotcache_amd.decode import chunks_per_page, decode_paged, make_plan
 
     clear_prepared_pools()
     rng = np.random.default_rng(hd + Q)
     for lens in ([64 * 9 + 17, 30, 64 * 4, 1000], [64 * 3 + 5, 64]):  # the second call is smaller
         case = _case(rng, lens, hd, Q, kfmt, vfmt)
-        plan = make_plan(case["counts"], 1, 2, device="cuda")  # 2 pages per split: partials and merges
-        assert plan.n_merges > 0
-        ref = decode_paged(case["kpool"], case["kt"], case["vt"], case["counts"], case["q"], plan=plan,
-                           v_pool=case["vpool"])
-        out = torch.full_like(ref, float("nan"))
-        _lib.check(_noalloc(case, plan, out), "dc_decode_paged_noalloc")
-        torch.cuda.synchronize()
-        assert torch.equal(out, ref), f"lens {lens}: max diff {(out - ref).abs().max().item()}"
-        assert np.max(np.abs(out.cpu().numpy()[:, 0] - case["want"])) < 3e-4
+        cpp = chunks_per_page(case["kpool"].geometry.page_capacity)
+        plans = {
+            "2 pages per split": make_plan(case["counts"], 1, 2, device="cuda"),
+            # items cut at 32-token chunks inside pages
+            "fill": make_plan(case["counts"], 1, device="cuda", target_items=7, chunks_per_page=cpp),
+        }
+        for name, plan in plans.items():
+            assert plan.n_merges > 0
+            ref = decode_paged(case["kpool"], case["kt"], case["vt"], case["counts"], case["q"], plan=plan,
+                               v_pool=case["vpool"])
+            out = torch.full_like(ref, float("nan"))
+            _lib.check(_noalloc(case, plan, out), "dc_decode_paged_noalloc")
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"lens {lens} plan {name}: max diff {(out - ref).abs().max().item()}"
+            assert np.max(np.abs(out.cpu().numpy()[:, 0] - case["want"])) < 3e-4
     clear_prepared_pools()
 
 
