@@ -14,6 +14,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib
+from .config import PageModeSpec, choose_page_mode, make_explicit_policy
 from .decode import DecodePlan, chunks_per_page, decode_paged, make_plan, merge_partials, page_costs, workspace_bytes
 from .page_pool import DevicePagePool, PoolGeometry
 
@@ -413,16 +414,25 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
 
 
 def _apply_recent_window(spec, k_pool, v_pool, kt, vt, n_pages, lengths, gen, dev, lt, layer):
-    """Replace the pages covering the newest ``recent_window`` tokens of each
-    sequence by fp16 (M3) pages holding fresh rows (the exact recent window)."""
+    """Replace the pages that the planner's recent-window rule keeps exact
+    (``choose_page_mode``: the page's oldest token is younger than
+    ``recent_window``, reference ``planner.py:84-106``) by fp16 (M3) pages
+    holding fresh rows."""
     torch = _torch()
     P = spec.page_size
     B, H = kt.shape[:2]
     hd = spec.head_dim
+    policy = {kind: make_explicit_policy(kind=kind, policy_id=f"{kind.lower()}_workload", sensitivity_tier="balanced",
+                                         candidates=(PageModeSpec(mode=fmt.mode, bits=fmt.bits,
+                                                                  quant_scheme=fmt.scheme),),
+                                         recent_window=spec.recent_window)
+              for kind, fmt in (("K", spec.key), ("V", spec.value))}
     for b in range(B):
         n = int(n_pages[b])
-        first = max(0, (int(lengths[b]) - spec.recent_window) // P)
-        for p in range(first, n):
+        exact = [p for p in range(n)
+                 if all(choose_page_mode(layer, kind, int(lengths[b]) - p * P - 1, None,
+                                         layer_policy=policy[kind]).mode == "M3" for kind in ("K", "V"))]
+        for p in exact:
             tokens = min(P, int(lengths[b]) - p * P)
             for pool, table in ((k_pool, kt), (v_pool, vt)):
                 ids = pool.allocate(_lib.FMT_M3_F16, 0, H, tokens=tokens)
