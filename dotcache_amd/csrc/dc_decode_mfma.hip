@@ -246,6 +246,15 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   using KB0 = std::integral_constant<int, 0>;
   using KB1 = std::integral_constant<int, 1>;
 
+  // The kernel arguments the prologue uses, read in one round of scalar
+  // loads at entry.  Read where each is first used, they were waited for one
+  // at a time along the dependent chain item -> page table -> descriptors
+  // (C3: 32.65 -> 32.35 us per launch).
+  asm volatile("" ::"s"(a.items), "s"(a.k_table), "s"(a.v_table), "s"(a.kpool.descs), "s"(a.vpool.descs),
+               "s"(a.kpool.arena), "s"(a.vpool.arena), "s"(a.queries), "s"(a.table_stride), "s"(a.n_seqs),
+               "s"(a.n_kv_heads), "s"(a.n_q), "s"(a.kpool.n_descs), "s"(a.vpool.n_descs),
+               "s"(a.kpool.geometry.page_capacity), "s"(a.queries_dtype), "s"(a.q_scale), "s"(a.kpool.arena_bytes),
+               "s"(a.vpool.arena_bytes));
   const dc_work_item it = a.items[blockIdx.x];
   if (!item_in_bounds(it, a)) return;
   const int lane = threadIdx.x;
