@@ -19,6 +19,10 @@ class PageDesc(C.Structure):
     _fields_ = [("block", C.c_uint32), ("tokens", C.c_uint16), ("format", C.c_uint8), ("bits", C.c_uint8)]
 
 
+class PageRecord(C.Structure):
+    _fields_ = [("key", PageDesc), ("value", PageDesc)]
+
+
 class PageGeometry(C.Structure):
     _fields_ = [("head_dim", C.c_int32), ("group_size", C.c_int32), ("page_capacity", C.c_int32), ("layout", C.c_int32)]
 
@@ -83,6 +87,12 @@ SIGNATURES = {
     "dc_decode_paged": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
                                   C.c_void_p, C.c_int32, C.c_float, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                   C.c_void_p, C.c_int64, C.c_void_p]),
+    "dc_gather_page_records": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
+                                         C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p]),
+    "dc_decode_paged_records": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
+                                          C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_float, C.c_int32,
+                                          C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,
+                                          C.c_int32, C.c_void_p]),
     "dc_decode_workspace_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32]),
     "dc_decode_paged_noalloc": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
                                           C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_float,

@@ -27,6 +27,10 @@ struct DecodeArgs {
   float* part_o;    // [max_partials][n_q][head_dim]
   float* part_ml;   // [max_partials][n_q][2]  (m, l) in the log2 domain
   int64_t max_partials;
+  // page records (dc_gather_page_records): [n_items][rec_stride] pairs of
+  // (key descriptor, value descriptor), or null
+  const dc_page_record* recs;
+  int32_t rec_stride;
 };
 
 // A work item naming a sequence, KV head or page range outside the call's

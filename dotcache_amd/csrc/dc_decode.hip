@@ -326,6 +326,27 @@ int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_mer
   return check_hip(hipGetLastError(), "merge_kernel launch");
 }
 
+// One thread per (item, record slot): the key and value descriptors of page
+// page_begin + slot of the item, read through its tables as the decode
+// kernels read them (an id outside a pool, or a slot past the item's pages,
+// gives a zero record).
+__global__ void __launch_bounds__(256) gather_records_kernel(DecodeArgs a, dc_page_record* recs) {
+  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= int64_t(a.n_items) * a.rec_stride) return;
+  const int32_t i = int32_t(e / a.rec_stride), slot = int32_t(e - int64_t(i) * a.rec_stride);
+  const dc_work_item it = a.items[i];
+  dc_page_record r{};
+  if (item_in_bounds(it, a) && slot < it.page_end - it.page_begin) {
+    const int64_t row = (int64_t(it.seq) * a.n_kv_heads + it.kv_head) * a.table_stride + it.page_begin + slot;
+    const int32_t kid = a.k_table[row], vid = a.v_table[row];
+    if (kid >= 0 && kid < a.kpool.n_descs && vid >= 0 && vid < a.vpool.n_descs) {
+      r.key = a.kpool.descs[kid];
+      r.value = a.vpool.descs[vid];
+    }
+  }
+  recs[e] = r;
+}
+
 }  // namespace dc
 
 extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table, int32_t table_stride,
@@ -333,6 +354,45 @@ extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_
                                int32_t n_merges, const void* queries, int32_t queries_dtype, float query_scale,
                                int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, float* out, void* workspace,
                                int64_t workspace_bytes, dc_stream_t stream) {
+  return dc_decode_paged_records(k_pool, v_pool, k_table, v_table, table_stride, items, n_items, merges, n_merges,
+                                 queries, queries_dtype, query_scale, n_seqs, n_kv_heads, n_q, out, workspace,
+                                 workspace_bytes, nullptr, 0, stream);
+}
+
+extern "C" int dc_gather_page_records(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table,
+                                      int32_t table_stride, const dc_work_item* items, int32_t n_items,
+                                      int32_t n_seqs, int32_t n_kv_heads, dc_page_record* records, int32_t rec_stride,
+                                      dc_stream_t stream) {
+  if (n_items < 0 || n_seqs <= 0 || n_kv_heads <= 0 || table_stride < 0 || rec_stride <= 0 || rec_stride > 64)
+    return dc::fail(DC_EINVAL, "dc_gather_page_records: bad sizes (rec_stride must be in [1, 64])");
+  if (n_items == 0) return DC_OK;
+  if (!k_table || !v_table || !items || !records || !k_pool.descs || !v_pool.descs)
+    return dc::fail(DC_EINVAL, "dc_gather_page_records: null pointer");
+  dc::DecodeArgs a{};
+  a.kpool = k_pool;
+  a.vpool = v_pool;
+  a.k_table = k_table;
+  a.v_table = v_table;
+  a.table_stride = table_stride;
+  a.items = items;
+  a.n_items = n_items;
+  a.n_seqs = n_seqs;
+  a.n_kv_heads = n_kv_heads;
+  a.rec_stride = rec_stride;
+  const int64_t n = int64_t(n_items) * rec_stride;
+  hipLaunchKernelGGL(dc::gather_records_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, hipStream_t(stream), a,
+                     records);
+  return dc::check_hip(hipGetLastError(), "gather_records_kernel launch");
+}
+
+extern "C" int dc_decode_paged_records(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table,
+                                       int32_t table_stride, const dc_work_item* items, int32_t n_items,
+                                       const dc_merge_item* merges, int32_t n_merges, const void* queries,
+                                       int32_t queries_dtype, float query_scale, int32_t n_seqs, int32_t n_kv_heads,
+                                       int32_t n_q, float* out, void* workspace, int64_t workspace_bytes,
+                                       const dc_page_record* records, int32_t rec_stride, dc_stream_t stream) {
+  if (records != nullptr && (rec_stride <= 0 || rec_stride > 64))
+    return dc::fail(DC_EINVAL, "dc_decode_paged_records: rec_stride must be in [1, 64]");
   if (int rc = dc::validate_geometry(k_pool.geometry)) return rc;
   if (int rc = dc::validate_geometry(v_pool.geometry)) return rc;
   const dc_page_geometry& g = k_pool.geometry;
@@ -377,6 +437,8 @@ extern "C" int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_
   a.part_o = reinterpret_cast<float*>(workspace);
   a.part_ml = a.part_o + n_partials * n_q * g.head_dim;
   a.max_partials = n_partials;
+  a.recs = records;
+  a.rec_stride = records ? rec_stride : 0;
   if (n_merges > 0 && (!workspace || n_partials <= 0))
     return dc::fail(DC_ESPACE, "dc_decode_paged: split-K items need a workspace");
 

@@ -254,7 +254,14 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
                "s"(a.kpool.arena), "s"(a.vpool.arena), "s"(a.queries), "s"(a.table_stride), "s"(a.n_seqs),
                "s"(a.n_kv_heads), "s"(a.n_q), "s"(a.kpool.n_descs), "s"(a.vpool.n_descs),
                "s"(a.kpool.geometry.page_capacity), "s"(a.queries_dtype), "s"(a.q_scale), "s"(a.kpool.arena_bytes),
-               "s"(a.vpool.arena_bytes));
+               "s"(a.vpool.arena_bytes), "s"(a.recs), "s"(a.rec_stride));
+  // With page records, lane i's record (the descriptors of the item's page
+  // i) is loaded together with the item: no dependence on it.
+  u32x4 rec = {0u, 0u, 0u, 0u};
+  if (a.recs != nullptr) {
+    const int slot = int(threadIdx.x) < a.rec_stride ? int(threadIdx.x) : a.rec_stride - 1;
+    rec = reinterpret_cast<const u32x4*>(a.recs)[int64_t(blockIdx.x) * a.rec_stride + slot];
+  }
   const dc_work_item it = a.items[blockIdx.x];
   if (!item_in_bounds(it, a)) return;
   const int lane = threadIdx.x;
@@ -312,8 +319,16 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
     const u32x2 vd = __builtin_amdgcn_raw_buffer_load_b64(vdr, ok ? int(uint32_t(vid) * 8u) : -16, 0, 0);
     k0 = kd.x; k1 = kd.y; v0 = vd.x; v1 = vd.y;
   };
-  if (np > 0) load_ids(0);
-  load_descs();  // unconditional: an empty item's lanes are not ok and read zeros
+  if (a.recs != nullptr && np <= a.rec_stride) {  // (rec_stride <= 64: one batch)
+    ok = lane < np;
+    k0 = ok ? rec.x : 0u;
+    k1 = ok ? rec.y : 0u;
+    v0 = ok ? rec.z : 0u;
+    v1 = ok ? rec.w : 0u;
+  } else {
+    if (np > 0) load_ids(0);
+    load_descs();  // unconditional: an empty item's lanes are not ok and read zeros
+  }
 
   // ---- queries scaled by query_scale * log2(e): B fragments hi / residual ----
   // converted once, after the item's first chunk loads are issued, so the

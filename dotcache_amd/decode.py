@@ -275,6 +275,54 @@ def set_mfma_head_block(nqb: int) -> None:
     _lib.check(_lib.lib().dc_set_mfma_head_block(int(nqb)), "dc_set_mfma_head_block")
 
 
+@dataclass
+class PageRecords:
+    """The key and value descriptors of every page of a plan's items
+    (``dc_gather_page_records``), so the MFMA kernel's waves skip the
+    page-table and descriptor reads before their first page loads.  A
+    snapshot of the plan, both tables and both pools' descriptors: stale,
+    and refused by :func:`decode_paged`, once any of them changes."""
+
+    data: object     # device uint8 tensor: n_items x stride x 16 bytes
+    stride: int      # records per item (items with more pages read the tables)
+    plan: DecodePlan
+    sources: tuple   # (k_table, v_table, key pool, value pool), held so their identities stay unique
+    versions: tuple  # the tables' and pools' versions at gather time
+
+    @staticmethod
+    def versions_of(k_table, v_table, pool, vpool) -> tuple:
+        return (int(k_table._version), int(v_table._version), int(pool.desc_version), int(vpool.desc_version))
+
+    def fresh_for(self, plan, k_table, v_table, pool, vpool) -> bool:
+        src = (k_table, v_table, pool, vpool)
+        return (self.plan is plan and all(a is b for a, b in zip(self.sources, src))
+                and self.versions == PageRecords.versions_of(*src))
+
+
+def gather_records(pool: DevicePagePool, k_table, v_table, seq_pages, plan: DecodePlan, *,
+                   v_pool: DevicePagePool | None = None, stride: int | None = None) -> PageRecords:
+    """Page records of ``plan`` over these tables (one launch of
+    ``dc_gather_page_records`` on the current stream): as many records per
+    item as its largest item has pages, at most ``stride`` (default and
+    limit 64); items with more pages read the tables."""
+    torch = _torch()
+    vpool = pool if v_pool is None else v_pool
+    B, H, stride_t = (int(x) for x in k_table.shape)
+    sp = np.asarray(seq_pages, dtype=np.int32)
+    plan.check(sp, H, stride_t, chunks_per_page(pool.geometry.page_capacity))
+    it = np.asarray(plan.host_items, dtype=np.int64).reshape(-1, 8)
+    pages = int(np.max(it[:, 3] - it[:, 2])) if len(it) else 1
+    rs = int(min(64 if stride is None else max(1, min(int(stride), 64)), max(1, pages)))
+    data = torch.empty(max(plan.n_items, 1) * rs * 16, dtype=torch.uint8, device=k_table.device)
+    st = _lib.lib().dc_gather_page_records(pool.c_pool(), vpool.c_pool(), C.c_void_p(k_table.data_ptr()),
+                                           C.c_void_p(v_table.data_ptr()), stride_t, C.c_void_p(plan.items.data_ptr()),
+                                           plan.n_items, B, H, C.c_void_p(data.data_ptr()), rs,
+                                           C.c_void_p(current_stream_ptr()))
+    _lib.check(st, "dc_gather_page_records")
+    return PageRecords(data, rs, plan, (k_table, v_table, pool, vpool),
+                       PageRecords.versions_of(k_table, v_table, pool, vpool))
+
+
 def workspace_bytes(plan: DecodePlan, n_q: int, head_dim: int) -> int:
     return int(_lib.lib().dc_decode_workspace_bytes(plan.n_partials, n_q, head_dim))
 
@@ -294,6 +342,7 @@ def decode_paged(
     validate: bool = True,
     v_pool: DevicePagePool | None = None,
     merge: bool = True,
+    records: PageRecords | None = None,
 ):
     """Fused decode for ``queries [n_seqs, n_kv_heads, n_q, head_dim]``.
 
@@ -304,7 +353,9 @@ def decode_paged(
     ``seq_pages[b]`` is the number of pages of sequence b (the first
     entries of its page-table rows).  ``merge=False`` leaves the split-K
     partials in ``workspace`` for :func:`merge_partials` (sequences that
-    were not split are written to ``out`` either way).
+    were not split are written to ``out`` either way).  ``records``: page
+    records of ``plan`` (:func:`gather_records`) over these tables and
+    pools; stale records raise ValueError.
     """
     torch = _torch()
     vpool = pool if v_pool is None else v_pool
@@ -346,14 +397,19 @@ def decode_paged(
     need = workspace_bytes(plan, Q, hd)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=queries.device)
-    st = _lib.lib().dc_decode_paged(
-        pool.c_pool(), vpool.c_pool(), C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
-        C.c_void_p(plan.items.data_ptr()), plan.n_items,
-        C.c_void_p(plan.merges.data_ptr() if plan.merges is not None and merge else 0), plan.n_merges if merge else 0,
-        C.c_void_p(queries.data_ptr()), dtype_code(queries), float(query_scale), B, H, Q,
-        C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()), int(workspace.numel()),
-        C.c_void_p(current_stream_ptr()),
-    )
+    args = (pool.c_pool(), vpool.c_pool(), C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
+            C.c_void_p(plan.items.data_ptr()), plan.n_items,
+            C.c_void_p(plan.merges.data_ptr() if plan.merges is not None and merge else 0),
+            plan.n_merges if merge else 0, C.c_void_p(queries.data_ptr()), dtype_code(queries), float(query_scale),
+            B, H, Q, C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()), int(workspace.numel()))
+    if records is None:
+        st = _lib.lib().dc_decode_paged(*args, C.c_void_p(current_stream_ptr()))
+    else:
+        if not records.fresh_for(plan, k_table, v_table, pool, vpool):
+            raise ValueError("page records are stale: gather them again after a change to the plan, the page "
+                             "tables or the pools' descriptors")
+        st = _lib.lib().dc_decode_paged_records(*args, C.c_void_p(records.data.data_ptr()), records.stride,
+                                                C.c_void_p(current_stream_ptr()))
     _lib.check(st, "dc_decode_paged")
     return out
 

@@ -123,6 +123,9 @@ class DevicePagePool:
         self._free_ids: deque[int] = deque()
         self._dev_desc = None
         self._dirty_ids: set[int] = set()  # descriptors changed since the last device upload
+        # bumped on every descriptor change: page records gathered at one
+        # version are stale at any other
+        self.desc_version = 0
         self.headers: dict[int, PageHeader] = {}
         self._blob_size: dict[int, int] = {}
         self._live = np.zeros(self._host_desc.shape[0], dtype=bool)
@@ -182,6 +185,7 @@ class DevicePagePool:
             self._blob_size[pid] = nblk
             ids[i] = pid
         self._dirty_ids.update(ids.tolist())
+        self.desc_version += 1
         return ids
 
     def free(self, page_ids) -> None:
@@ -196,6 +200,7 @@ class DevicePagePool:
             self.headers.pop(pid, None)
             self._dirty_ids.add(pid)
             self._free_ids.append(pid)
+            self.desc_version += 1
 
     def set_tokens(self, page_ids, tokens) -> None:
         ids = np.atleast_1d(np.asarray(page_ids, dtype=np.int64)).ravel()
@@ -208,6 +213,7 @@ class DevicePagePool:
             if h is not None:
                 h.token_count = int(t)
         self._dirty_ids.update(ids.tolist())
+        self.desc_version += 1
 
     def desc(self, page_id: int):
         return self._host_desc[int(page_id)]
@@ -322,6 +328,7 @@ class DevicePagePool:
                 self._blob_size[pid] = nblk
                 self.headers[pid] = PageHeader.from_dict(pages[i].header.to_dict())
                 self._dirty_ids.add(pid)
+                self.desc_version += 1
                 ids[i] = pid
             if n_old == 0:  # fresh contiguous blocks: one copy
                 self.arena[start * 256: start * 256 + host.size].copy_(src, non_blocking=False)

@@ -15,7 +15,8 @@ import numpy as np
 
 from . import _lib
 from .config import PageModeSpec, choose_page_mode, make_explicit_policy
-from .decode import DecodePlan, chunks_per_page, decode_paged, make_plan, merge_partials, page_costs, workspace_bytes
+from .decode import (DecodePlan, chunks_per_page, decode_paged, gather_records, make_plan, merge_partials,
+                     page_costs, workspace_bytes)
 from .page_pool import DevicePagePool, PoolGeometry
 
 
@@ -127,6 +128,7 @@ class Workload:
     new_v: list = field(default_factory=list)
     plan: DecodePlan | None = None  # layer 0's plan (every layer's when a split is given)
     plans: list = field(default_factory=list)  # per layer: items of near-equal cost under its page formats
+    records: list = field(default_factory=list)  # per layer: page records of its plan (PageRecords)
     outs: list = field(default_factory=list)
     workspace: object = None
     k_page_ids_by_layer: list = field(default_factory=list)
@@ -198,12 +200,17 @@ class Workload:
         merge_partials(self.plans[l], self.outs[l], self.workspace)
 
     def decode_kernel(self, l: int) -> None:
-        """Layer ``l``'s decode kernel alone (``dc_decode_paged`` without
-        the merge)."""
+        """Layer ``l``'s decode kernel alone (``dc_decode_paged_records``
+        without the merge).  The layer's page records are gathered again
+        first if its tables or the pools changed since."""
         lt = self.layers[l]
+        rec = self.records[l] if self.records else None
+        if rec is not None and not rec.fresh_for(self.plans[l], lt.k_table, lt.v_table, self.k_pool, self.v_pool):
+            rec = self.records[l] = gather_records(self.k_pool, lt.k_table, lt.v_table, lt.seq_pages, self.plans[l],
+                                                   v_pool=self.v_pool)
         decode_paged(self.k_pool, lt.k_table, lt.v_table, lt.seq_pages, self.queries[l],
                      query_scale=self.query_scale, plan=self.plans[l], out=self.outs[l], workspace=self.workspace,
-                     validate=False, v_pool=self.v_pool, merge=False)
+                     validate=False, v_pool=self.v_pool, merge=False, records=rec)
 
     def capture(self) -> None:
         """Capture one whole step (every layer's append, decode and merge
@@ -409,6 +416,11 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
         wl.slot_dev = torch.zeros(B * H, dtype=torch.int32, device=dev)
     k_pool.device_descs()
     v_pool.device_descs()
+    # the descriptors of every item's pages, gathered once: the tables and
+    # descriptors stay fixed from here on (the append writes a tail page's
+    # codes, not its descriptor)
+    wl.records = [gather_records(k_pool, lt.k_table, lt.v_table, lt.seq_pages, wl.plans[l], v_pool=v_pool)
+                  for l, lt in enumerate(tables)]
     torch.cuda.synchronize(dev)
     return wl
 

@@ -70,6 +70,13 @@ typedef struct dc_page_desc {
   uint8_t bits;    /* M0 code width: 2, 3, 4 or 8 (ignored for M3)         */
 } dc_page_desc;
 
+/* The key and value descriptors of one page of a work item, gathered ahead
+ * of a decode (dc_gather_page_records). */
+typedef struct dc_page_record {
+  dc_page_desc key;
+  dc_page_desc value;
+} dc_page_record;
+
 /* Geometry shared by every page of one call (one layer's pages). */
 typedef struct dc_page_geometry {
   int32_t head_dim;
@@ -315,6 +322,35 @@ int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, cons
                     int32_t n_seqs, int32_t n_kv_heads, int32_t n_q,
                     float* out, void* workspace, int64_t workspace_bytes,
                     dc_stream_t stream);
+
+/* Page records for a plan: records[i * rec_stride + s] receives the key and
+ * value descriptors of page page_begin + s of work item i, read through
+ * k_table / v_table (zeros past the item's pages, or for an id outside
+ * its pool).  1 <= rec_stride <= 64.  A snapshot: it stays valid while the
+ * items, the tables' entries for those pages and the pools' descriptors of
+ * those pages do not change; gather again after any change (an append
+ * that changes a page's token count included).  No reference counterpart:
+ * it moves the page-table and descriptor reads of the reference's chunked
+ * decode (dotcache/backends/torch_mps.py:4110-4273) out of the decode
+ * launch, so a decode's waves issue their first page loads one dependent
+ * load after their start instead of three. */
+int dc_gather_page_records(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table,
+                           int32_t table_stride, const dc_work_item* items, int32_t n_items, int32_t n_seqs,
+                           int32_t n_kv_heads, dc_page_record* records, int32_t rec_stride, dc_stream_t stream);
+
+/* dc_decode_paged with the page records of its items (from
+ * dc_gather_page_records with the same items, tables and descriptors, and
+ * the same rec_stride).  The MFMA kernel reads the descriptors of an item
+ * of at most rec_stride pages from its records instead of through the
+ * tables; other items, and the generic kernel, read the tables.  records
+ * NULL: exactly dc_decode_paged.  Replaces the same reference functions as
+ * dc_decode_paged. */
+int dc_decode_paged_records(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table,
+                            int32_t table_stride, const dc_work_item* items, int32_t n_items,
+                            const dc_merge_item* merges, int32_t n_merges, const void* queries,
+                            int32_t queries_dtype, float query_scale, int32_t n_seqs, int32_t n_kv_heads,
+                            int32_t n_q, float* out, void* workspace, int64_t workspace_bytes,
+                            const dc_page_record* records, int32_t rec_stride, dc_stream_t stream);
 
 int64_t dc_decode_workspace_bytes(int32_t n_partials, int32_t n_q, int32_t head_dim);
 

@@ -310,3 +310,16 @@ def test_page_costs_weigh_pages_within_a_stream():
     np.testing.assert_allclose(c[0, 0], raw * 4 / raw.sum(), rtol=1e-6)
     assert c[0, 0, 3] > 1.3 * c[0, 0, 0]  # the exact page reads 16 KiB of keys instead of 5
     np.testing.assert_allclose(c[1, 0], [1.0, 0.0, 0.0, 0.0])
+
+
+def test_page_record_calls_reject_bad_strides():
+    """dc_gather_page_records and dc_decode_paged_records check rec_stride
+    (1..64) before touching the device."""
+    L = _lib.lib()
+    geo = _lib.geometry(128, 32, 64)
+    pool = _lib.Pool(None, 0, None, 0, geo, 0)
+    assert C.sizeof(_lib.PageRecord) == 16
+    for bad in (0, 65):
+        assert L.dc_gather_page_records(pool, pool, None, None, 1, None, 1, 1, 1, None, bad, None) == _lib.DC_EINVAL
+        assert L.dc_decode_paged_records(pool, pool, None, None, 1, None, 1, None, 0, None, _lib.DT_F32, 1.0, 1, 1,
+                                         1, None, None, 0, C.c_void_p(16), bad, None) == _lib.DC_EINVAL

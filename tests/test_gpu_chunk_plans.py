@@ -169,3 +169,41 @@ def test_single_page_items_and_empty_items():
                       chunks_per_page=cpp)
     err = float(np.max(np.abs(_decode(case, plan) - case["want"])))
     assert err < KERNEL_TOL, f"max-abs error {err}"
+
+
+@pytest.mark.parametrize("kfmt,vfmt,vgs,hd,Q,tpp", CASES[:3])
+def test_page_records_give_the_same_outputs(kfmt, vfmt, vgs, hd, Q, tpp):
+    """Decode with page records (every item's descriptors gathered ahead)
+    equals the decode through the tables bit for bit, with records covering
+    every item or only the items of at most 3 pages; records go stale when
+    a table or a pool's descriptors change."""
+    import torch
+
+    from dotcache_amd.decode import chunks_per_page, decode_paged, gather_records, make_plan
+
+    rng = np.random.default_rng(500 + hd)
+    case = _case(rng, [tpp * 9 - 5, tpp * 70 + 1, 33, 1], hd, Q, tpp, kfmt, vfmt, vgs, empty_at=(1, 66))
+    counts = case["counts"]
+    cpp = chunks_per_page(case["kpool"].geometry.page_capacity)
+    args = (case["kpool"], case["kt"], case["vt"], counts)
+    for plan in (make_plan(counts, 1, device="cuda", target_items=23, chunks_per_page=cpp),
+                 make_plan(counts, 1, 3, device="cuda")):
+        want = decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"]).clone()
+        for stride in (None, 3):
+            rec = gather_records(*args, plan, v_pool=case["vpool"], stride=stride)
+            got = decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"], records=rec)
+            assert torch.equal(got, want), f"stride {stride}: max diff {(got - want).abs().max().item()}"
+            assert np.max(np.abs(got.cpu().numpy()[:, 0] - case["want"])) < KERNEL_TOL
+    # stale: another plan, a table written in place, a pool's descriptors changed
+    rec = gather_records(*args, plan, v_pool=case["vpool"])
+    other = make_plan(counts, 1, 2, device="cuda")
+    with pytest.raises(ValueError):
+        decode_paged(*args, case["q"], plan=other, v_pool=case["vpool"], records=rec)
+    case["kt"][0, 0, 0] = case["kt"][0, 0, 0]
+    with pytest.raises(ValueError):
+        decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"], records=rec)
+    rec = gather_records(*args, plan, v_pool=case["vpool"])
+    pid = int(case["kt"][2, 0, 0].item())
+    case["kpool"].set_tokens([pid], case["kpool"].tokens_of([pid]))
+    with pytest.raises(ValueError):
+        decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"], records=rec)
