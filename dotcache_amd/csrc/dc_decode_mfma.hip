@@ -11,6 +11,10 @@
 // up to 16 query heads per KV head.  Other formats take the generic kernel
 // (dc_decode.hip).
 //
+// Prologue: the item, then its pages' table entries, then their
+// descriptors -- or, with page records (dc_gather_page_records), the item
+// and its pages' descriptors in one round, indexed by the workgroup id.
+//
 // Pipeline (head_dim <= 128, pools without M3 values): while chunk j is
 // mixed, chunk j + 1 is staged and scored and chunk j + 2 is being loaded,
 // so the score's MFMA chain, the mix's unpacking and the loads of one
