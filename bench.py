@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--pages-per-split", type=int, default=None)
+    ap.add_argument("--no-page-records", action="store_true",
+                    help="decode through the page tables instead of page records gathered ahead")
     ap.add_argument("--contiguous-pages", action="store_true",
                     help="keep each sequence's pages in allocation order instead of scattering them over the pool")
     ap.add_argument("--decode-path", default="auto", choices=["auto", "generic", "mfma"],
@@ -308,6 +310,8 @@ def main():
     # "fill": per-layer plans of a launch's item budget cut at 32-token chunks
     # by page cost; "pages": --pages-per-split whole-page splits
     plan_kind = "fill" if args.pages_per_split is None else "pages"
+    if args.no_page_records:
+        wl.records = []
     log(f"built in {time.time() - t0:.1f} s: {wl.plan.n_items} work items/layer, pages/split {wl.plan.pages_per_split}, "
         f"K pool {wl.k_pool.arena.numel() / 1e9:.2f} GB, V pool {wl.v_pool.arena.numel() / 1e9:.2f} GB")
 
@@ -442,6 +446,7 @@ def main():
             "value_pages": fmt(spec.value),
             "append": spec.append,
             "plan": plan_kind,
+            "page_records": bool(wl.records),
             "pages_per_split": wl.plan.pages_per_split,
             "launch": "eager" if args.eager else "hip graph of the whole step",
             "parallelism": "single GPU",
