@@ -93,6 +93,7 @@ SIGNATURES = {
                                           C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_float, C.c_int32,
                                           C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,
                                           C.c_int32, C.c_void_p]),
+    "dc_decode_waves_per_simd": (C.c_int32, [Pool, Pool, C.c_int32]),
     "dc_decode_workspace_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32]),
     "dc_decode_paged_noalloc": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
                                           C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_float,

@@ -29,7 +29,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from .config import DotCacheConfig
-from .decode import chunks_per_page, decode_paged, make_plan, workspace_bytes
+from .decode import chunks_per_page, decode_paged, launch_target_items, make_plan, workspace_bytes
 from .encode import resolve_encode_spec
 from .kv_cache import default_q_head_to_kv_head
 from .page_pool import DevicePagePool, PoolGeometry, page_format_of
@@ -278,7 +278,8 @@ class DeviceVllmPagedKVCache:
         qg = (q if contiguous else q[:, order_t]).reshape(B, H, Hq // H, hd)
         seq_pages = n_blocks.astype(np.int32)
         plan = make_plan(seq_pages, H, device=self.device,
-                         chunks_per_page=chunks_per_page(self.k_pool.geometry.page_capacity))
+                         chunks_per_page=chunks_per_page(self.k_pool.geometry.page_capacity),
+                         target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H))
         need = workspace_bytes(plan, Hq // H, hd)
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.device)

@@ -54,6 +54,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 int launch_decode(const DecodeArgs& a, hipStream_t stream);
+int decode_mfma_waves(const DecodeArgs& a);
 int launch_decode_generic(const DecodeArgs& a, hipStream_t stream);
 // Launches the MFMA kernel when every format in the pools' masks and the
 // geometry fit it; *launched tells the caller whether to fall back.

@@ -470,6 +470,17 @@ extern "C" int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const
   return dc::launch_merge(a, merges, n_merges, hipStream_t(stream));
 }
 
+extern "C" int32_t dc_decode_waves_per_simd(dc_pool k_pool, dc_pool v_pool, int32_t n_q) {
+  if (n_q <= 0 || n_q > dc::kMaxQ) return 1;
+  dc::DecodeArgs a{};
+  a.kpool = k_pool;
+  a.vpool = v_pool;
+  a.n_q = n_q;
+  if (dc::g_decode_path == 1) return 1;
+  const int w = dc::decode_mfma_waves(a);
+  return w > 0 ? w : 1;
+}
+
 extern "C" int dc_set_decode_path(int32_t path) {
   if (path < 0 || path > 2) return dc::fail(DC_EINVAL, "decode path must be 0 (auto), 1 (generic) or 2 (mfma)");
   dc::g_decode_path = path;

@@ -149,10 +149,23 @@ struct MfmaCfg {
   static_assert(W % 4 == 0, "value code rows are staged in 16-byte pieces");
 };
 
-// Two staged chunks in flight where the registers allow it.
-template <int HD, int KMODE, bool VM3>
+// Waves per SIMD an instance is built for.  Pools with M0 keys at
+// head_dim 128 and up to 8 heads per block are bound by instruction issue:
+// two unpipelined waves per SIMD (at most 256 registers each) hide each
+// other's waits, where one pipelined wave cannot (C4: 42.1 against 49.3 us
+// per launch).  Pools of M3 keys (C3) stream bytes and keep one pipelined
+// wave (two waves: 32.9 against 32.7 us).
+template <int HD, int KMODE, int KBITS, int VBITS, int NQB>
+constexpr int waves_per_simd() {
+  // (8-bit keys and values with 8 heads per block spill at 256 registers)
+  return HD == 128 && KMODE != KEYS_M3 && NQB <= 8 && !(KBITS == 8 && VBITS == 8 && NQB == 8) ? 2 : 1;
+}
+
+// Two staged chunks in flight where the registers allow it: one wave per
+// SIMD, head_dim <= 128, no M3 values, one key format.
+template <int HD, int KMODE, int KBITS, int VBITS, bool VM3, int NQB>
 constexpr bool pipelined() {
-  return HD <= 128 && !VM3;
+  return HD <= 128 && !VM3 && KMODE != KEYS_MIXED && waves_per_simd<HD, KMODE, KBITS, VBITS, NQB>() == 1;
 }
 
 // Registers one chunk needs from HBM.  Keys: with ROWS (pools of mixed key
@@ -202,10 +215,11 @@ struct PageMeta {
 // heads, and copy c works on group c of each block of GB consecutive
 // groups (see "Group blocks" above).
 template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF, int NQB>
-__global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, NQB>()))
+    decode_mfma_kernel(DecodeArgs a) {
   static_assert(KBITS == 4 || KBITS == 8, "M0 keys are 4- or 8-bit");
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  constexpr bool kPipe = pipelined<HD, KMODE, VM3>();
+  constexpr bool kPipe = pipelined<HD, KMODE, KBITS, VBITS, VM3, NQB>();
   // mixed key formats with chunks in flight: key rows / code pieces in registers
   constexpr bool kRowRegs = KMODE == KEYS_MIXED && kPipe;
   // Chunk-loop specialisations: FM_ANY takes every format the pool allows,
@@ -1250,8 +1264,13 @@ __global__ void __launch_bounds__(64, 1) decode_mfma_kernel(DecodeArgs a) {
   }
 }
 
+// Set while dc_decode_waves_per_simd walks the instance selection: the
+// instance's launcher then reports its waves per SIMD instead of launching.
+static thread_local bool g_query_waves = false;
+
 template <int HD, int VGS, int KMODE, int KBITS, int VBITS, bool VM3, bool KAFF, bool VAFF, int NQB = 16>
 static int launch_t(const DecodeArgs& a, hipStream_t stream) {
+  if (g_query_waves) return waves_per_simd<HD, KMODE, KBITS, VBITS, NQB>();
   hipLaunchKernelGGL((decode_mfma_kernel<HD, VGS, KMODE, KBITS, VBITS, VM3, KAFF, VAFF, NQB>),
                      dim3(uint32_t(a.n_items)), dim3(64), 0, stream, a);
   return check_hip(hipGetLastError(), "decode_mfma_kernel launch");
@@ -1335,6 +1354,16 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   if (rc < 0) return DC_OK;
   *launched = true;
   return rc;
+}
+
+// Waves per SIMD of the MFMA instance a decode with these pools and n_q
+// would launch (0: the MFMA kernel does not take them).
+int decode_mfma_waves(const DecodeArgs& a) {
+  bool launched = false;
+  g_query_waves = true;
+  const int w = launch_decode_mfma(a, nullptr, &launched);
+  g_query_waves = false;
+  return launched ? w : 0;
 }
 
 }  // namespace dc

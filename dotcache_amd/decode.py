@@ -124,6 +124,19 @@ def default_target_items() -> int:
     return DEFAULT_TARGET_ITEMS
 
 
+def waves_per_simd(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q: int) -> int:
+    """Work items per SIMD the decode kernel for these pools and ``n_q``
+    runs at once (``dc_decode_waves_per_simd``): 1 or 2."""
+    vpool = pool if v_pool is None else v_pool
+    return int(_lib.lib().dc_decode_waves_per_simd(pool.c_pool(), vpool.c_pool(), int(n_q)))
+
+
+def launch_target_items(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q: int) -> int:
+    """Items that fill one launch round: one per SIMD times the kernel's
+    waves per SIMD."""
+    return default_target_items() * waves_per_simd(pool, v_pool, n_q)
+
+
 def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items: int | None = None) -> int:
     """Smallest pages-per-split (at least MIN_PAGES_PER_SPLIT) for which the
     plan has at most ``target_items`` items; the planner then cuts every
@@ -388,7 +401,8 @@ def decode_paged(
                 raise ValueError("key and value pages must hold the same token counts")
     cpp = chunks_per_page(pool.geometry.page_capacity)
     if plan is None:
-        plan = make_plan(sp, H, pages_per_split, device=queries.device, chunks_per_page=cpp)
+        plan = make_plan(sp, H, pages_per_split, device=queries.device, chunks_per_page=cpp,
+                         target_items=launch_target_items(pool, vpool, Q))
     plan.check(sp, H, stride, cpp)
     if not queries.is_contiguous():
         queries = queries.contiguous()

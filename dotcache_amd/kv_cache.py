@@ -35,7 +35,7 @@ from __future__ import annotations
 import numpy as np
 
 from .config import DotCacheConfig, observe_page
-from .decode import chunks_per_page, decode_paged, make_plan, workspace_bytes
+from .decode import chunks_per_page, decode_paged, launch_target_items, make_plan, workspace_bytes
 from .encode import make_header, resolve_encode_spec
 from .page_pool import DevicePagePool, PoolGeometry, page_format_of
 
@@ -294,7 +294,8 @@ class DevicePagedKVCache:
         qg = q if contiguous else q[:, torch.from_numpy(order).to(self.device)]
         queries = qg.reshape(B, H, Hq // H, hd)
         plan = make_plan(seq_pages, H, device=self.device,
-                         chunks_per_page=chunks_per_page(self.k_pool.geometry.page_capacity))
+                         chunks_per_page=chunks_per_page(self.k_pool.geometry.page_capacity),
+                         target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H))
         need = workspace_bytes(plan, Hq // H, hd)
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.device)

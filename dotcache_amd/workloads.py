@@ -15,8 +15,8 @@ import numpy as np
 
 from . import _lib
 from .config import PageModeSpec, choose_page_mode, make_explicit_policy
-from .decode import (DecodePlan, chunks_per_page, decode_paged, gather_records, make_plan, merge_partials,
-                     page_costs, workspace_bytes)
+from .decode import (DecodePlan, chunks_per_page, decode_paged, gather_records, launch_target_items, make_plan,
+                     merge_partials, page_costs, workspace_bytes)
 from .page_pool import DevicePagePool, PoolGeometry
 
 
@@ -405,7 +405,8 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
         cost = None
         if pages_per_split is None:
             cost = page_costs(k_pool, v_pool, kids_tables[l], vids_tables[l], lt.seq_pages)
-        wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp, page_cost=cost))
+        wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp, page_cost=cost,
+                                  target_items=launch_target_items(k_pool, v_pool, Q)))
     wl.plan = wl.plans[0]
     need = max(workspace_bytes(p, Q, hd) for p in wl.plans)
     wl.workspace = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)

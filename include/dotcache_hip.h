@@ -323,6 +323,13 @@ int dc_decode_paged(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, cons
                     float* out, void* workspace, int64_t workspace_bytes,
                     dc_stream_t stream);
 
+/* Work items per SIMD that the decode kernel chosen for these pools and
+ * n_q runs at once: 2 for the MFMA kernel's instances built for two waves
+ * per SIMD (M0 keys at head_dim 128, up to 8 heads per block), else 1.  A
+ * planner fills a launch with this many items per SIMD (dc_plan_decode_fill's
+ * target_items).  No reference counterpart. */
+int32_t dc_decode_waves_per_simd(dc_pool k_pool, dc_pool v_pool, int32_t n_q);
+
 /* Page records for a plan: records[i * rec_stride + s] receives the key and
  * value descriptors of page page_begin + s of work item i, read through
  * k_table / v_table (zeros past the item's pages, or for an id outside

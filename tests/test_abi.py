@@ -323,3 +323,38 @@ def test_page_record_calls_reject_bad_strides():
         assert L.dc_gather_page_records(pool, pool, None, None, 1, None, 1, 1, 1, None, bad, None) == _lib.DC_EINVAL
         assert L.dc_decode_paged_records(pool, pool, None, None, 1, None, 1, None, 0, None, _lib.DT_F32, 1.0, 1, 1,
                                          1, None, None, 0, C.c_void_p(16), bad, None) == _lib.DC_EINVAL
+
+
+def test_waves_per_simd_follows_the_instance():
+    """dc_decode_waves_per_simd walks the MFMA kernel's instance selection
+    without launching: 2 for M0 keys at head_dim 128 with up to 8 heads per
+    block (C4's pools), 1 for M3 keys (C3), head_dim 256 (C5), 16-head
+    blocks, and the generic kernel."""
+    from dotcache_amd.decode import set_decode_path, set_mfma_head_block
+
+    L = _lib.lib()
+
+    def pool(hd, gs, masks):
+        m = 0
+        for fmt, bits in masks:
+            m |= _lib.format_bit(fmt, bits)
+        return _lib.Pool(None, 0, None, 0, _lib.geometry(hd, gs, 64), m)
+
+    m3, aff4, sym4, sym8 = (_lib.FMT_M3_F16, 0), (_lib.FMT_M0_AFFINE, 4), (_lib.FMT_M0_SYMMETRIC, 4), (
+        _lib.FMT_M0_SYMMETRIC, 8)
+    c4 = (pool(128, 32, [m3, aff4]), pool(128, 64, [sym8]))
+    c3 = (pool(128, 32, [m3]), pool(128, 32, [sym4]))
+    c5 = (pool(256, 32, [m3, aff4]), pool(256, 32, [m3, aff4]))
+    try:
+        assert L.dc_decode_waves_per_simd(*c4, 6) == 2
+        assert L.dc_decode_waves_per_simd(*c4, 12) == 1  # a 16-head block
+        assert L.dc_decode_waves_per_simd(*c3, 7) == 1
+        assert L.dc_decode_waves_per_simd(*c5, 4) == 1
+        set_mfma_head_block(16)
+        assert L.dc_decode_waves_per_simd(*c4, 6) == 1
+        set_mfma_head_block(0)
+        set_decode_path("generic")
+        assert L.dc_decode_waves_per_simd(*c4, 6) == 1
+    finally:
+        set_decode_path("auto")
+        set_mfma_head_block(0)
