@@ -15,12 +15,13 @@
 // descriptors -- or, with page records (dc_gather_page_records), the item
 // and its pages' descriptors in one round, indexed by the workgroup id.
 //
-// Pipeline (head_dim <= 128, pools without M3 values): while chunk j is
-// mixed, chunk j + 1 is staged and scored and chunk j + 2 is being loaded,
-// so the score's MFMA chain, the mix's unpacking and the loads of one
-// wavefront overlap.  Other pools keep one chunk in flight.  M3 key and
-// value rows reach LDS by DMA (buffer_load ... lds), except in pipelined
-// pools of mixed key formats, which load 16-byte key pieces into registers.
+// Pipeline (one wave per SIMD, head_dim <= 128, one key format, no M3
+// values): while chunk j is mixed, chunk j + 1 is staged and scored and
+// chunk j + 2 is being loaded, so the score's MFMA chain, the mix's
+// unpacking and the loads of one wavefront overlap.  Other pools keep one
+// chunk in flight (instances built for two waves per SIMD overlap across
+// waves instead).  M3 key and value rows reach LDS by DMA
+// (buffer_load ... lds).
 //
 // Exactness.  Every MFMA operand is exact: escape rows are fp16 already,
 // codes minus zero point are small integers, and each fp32 operand (scaled
@@ -168,17 +169,14 @@ constexpr bool pipelined() {
   return HD <= 128 && !VM3 && KMODE != KEYS_MIXED && waves_per_simd<HD, KMODE, KBITS, VBITS, NQB>() == 1;
 }
 
-// Registers one chunk needs from HBM.  Keys: with ROWS (pools of mixed key
-// formats with chunks in flight) 16 bytes per (tile, group), an M3 row piece
-// or the 16-byte aligned piece of the M0 code block that holds this lane's
-// words; otherwise this lane's KW words of each M0 code block, and M3 rows
-// go straight to LDS.
-template <int HD, int VGS, int VBITS, int KMODE, int KBITS, bool ROWS>
+// Registers one chunk needs from HBM: this lane's KW words of each M0 key
+// code block (M3 key rows go straight to LDS), the value code pieces and
+// the scale / bias words.
+template <int HD, int VGS, int VBITS, int KMODE, int KBITS>
 struct ChunkRegs {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  static constexpr bool kKeyWords = KMODE != KEYS_M3 && !ROWS;
+  static constexpr bool kKeyWords = KMODE != KEYS_M3;
   static constexpr int KW = KBITS / 4;  // code words of one lane's 8 channels
-  u32x4 kr[ROWS ? 2 : 1][ROWS ? Cfg::KG : 1];
   uint32_t kw[kKeyWords ? 2 : 1][kKeyWords ? Cfg::KG * KW : 1];
   u32x4 vr[Cfg::NVP];  // value code pieces, blob byte order
   uint32_t ks[Cfg::NKS], kbw[Cfg::NKS], vs[Cfg::NVS], vb[Cfg::NVS];  // scale / bias words
@@ -220,17 +218,6 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   static_assert(KBITS == 4 || KBITS == 8, "M0 keys are 4- or 8-bit");
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
   constexpr bool kPipe = pipelined<HD, KMODE, KBITS, VBITS, VM3, NQB>();
-  // mixed key formats with chunks in flight: key rows / code pieces in registers
-  constexpr bool kRowRegs = KMODE == KEYS_MIXED && kPipe;
-  // Chunk-loop specialisations: FM_ANY takes every format the pool allows,
-  // checked per chunk; FM_M0 serves a batch of pages whose keys and values
-  // are all M0 (nearly every batch of a mixed pool), with the M3 paths and
-  // their registers compiled out.  Pipelined mixed pools get both (C4-like
-  // pools: 49.7 against 51.4 us); one chunk in flight (head_dim 256 with an
-  // fp16 window) measured no faster with both.
-  using FM_ANY = std::integral_constant<bool, false>;
-  using FM_M0 = std::integral_constant<bool, true>;
-  constexpr bool kTwoLoops = KMODE == KEYS_MIXED && kPipe;
   constexpr int KBLK = 4 * KBITS;  // bytes of one (token, group) key code block
   constexpr int KG = Cfg::KG, VG = Cfg::VG, H = Cfg::H, LPW4 = Cfg::LPW4, W = Cfg::W, NACC = Cfg::NACC;
   static_assert(NQB == 4 || NQB == 8 || NQB == 16, "4, 8 or 16 heads per block");
@@ -244,7 +231,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   // instruction, and the score reads them back in the MFMA's A layout, with
   // the slot swizzle key_swz.  One buffer per chunk in flight, as separate
   // objects, so a read of one waits only for its own loads.
-  constexpr bool kDmaK = KMODE != KEYS_M0 && !kRowRegs;
+  constexpr bool kDmaK = KMODE != KEYS_M0;
   // pools with 4-bit M0 keys order each lane's 8 channels as pairs (i, i + 4)
   constexpr bool kPairedQ = KMODE != KEYS_M3 && KBITS == 4;
   __shared__ __attribute__((aligned(16))) uint32_t kbuf0[kDmaK ? 32 * HD / 2 : 1];
@@ -446,9 +433,9 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   asm volatile("" : "+v"(fp16_magic));
 
 
-  auto key_is_m3 = [&](const PageMeta& m, auto fm) -> bool {
+  auto key_is_m3 = [&](const PageMeta& m) -> bool {
     if constexpr (KMODE == KEYS_M3) return true;
-    if constexpr (KMODE == KEYS_M0 || decltype(fm)::value) return false;
+    if constexpr (KMODE == KEYS_M0) return false;
     return m.kfmt == DC_FMT_M3_F16;
   };
 
@@ -462,18 +449,6 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   uint32_t koff_m0[2];
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) koff_m0[hh] = (8 * (r >> 2) + 4 * hh + (r & 3)) * KBLK + KBITS * kb;
-  // key registers by rows: the M3 row piece (channels 8 kb .. 8 kb + 7 of
-  // group 0), or 16 bytes of M0 codes that start at the lane's words; the
-  // chunk's last row (token 31: tile 1, r = 15) ends them at the lane's words
-  // instead, so no load reaches into the next chunk
-  const bool last_row = r == 15;
-  uint32_t koff_m3[2], koff_a[2];
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const uint32_t ta = 8 * (r >> 2) + 4 * hh + (r & 3);
-    koff_m3[hh] = (ta * HD + 8 * kb) * 2;
-    koff_a[hh] = ta * KBLK + KBITS * kb - (hh == 1 && last_row ? 16u - KBITS : 0u);
-  }
   // key DMA: rows of PPR pieces, RPI rows per instruction, NDMA instructions
   // per chunk; instruction i writes rows RPI i .. RPI i + RPI - 1, lane l slot
   // l % PPR of row RPI i + l / PPR, from source piece (l % PPR) ^ key_swz(row).
@@ -522,10 +497,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   }
   const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
-  auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi, auto fm) __attribute__((always_inline)) {
-    constexpr bool M0O = decltype(fm)::value;
-    constexpr int KM = M0O ? KEYS_M0 : KMODE;
-    constexpr bool ROWS = kRowRegs && !M0O;
+  auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi) __attribute__((always_inline)) {
     const int c0 = m.c0;
     auto dma_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
       const uint32_t l = KMODE == KEYS_M3 ? 0u : fresh_lane();
@@ -564,33 +536,11 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
           R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(ksoff), kbs + c0 * KG * 2 + 256 * k, kNT);
       }
     };
-    if constexpr (ROWS) {
-      // both formats through the same loads (wave-uniform offsets), so every
-      // chunk issues the same loads and the compiler's counts of loads in
-      // flight stay exact across chunks of either format
-      const bool km3 = key_is_m3(m, fm);
-      const int cbase = c0 * (km3 ? HD * 2 : KBLK);
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const uint32_t lo = km3 ? koff_m3[hh] : koff_a[hh];
-#pragma unroll
-        for (int g = 0; g < KG; ++g) {
-          const int goff = km3 ? 64 * g : g * CAP * KBLK;
-          R.kr[hh][g] = __builtin_amdgcn_raw_buffer_load_b128(m.krs, int(lo), cbase + goff, kNT);
-        }
-      }
-      const int ksc = __builtin_amdgcn_readfirstlane(int(m.ksc)), kbs = __builtin_amdgcn_readfirstlane(int(m.kbs));
-#pragma unroll
-      for (int k = 0; k < Cfg::NKS; ++k) {
-        R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), ksc + c0 * KG * 2 + 256 * k, kNT);
-        if constexpr (KAFF)
-          R.kbw[k] = __builtin_amdgcn_raw_buffer_load_b32(m.krs, int(ksoff), kbs + c0 * KG * 2 + 256 * k, kNT);
-      }
-    } else if constexpr (KM == KEYS_M3) {
+    if constexpr (KMODE == KEYS_M3) {
       dma_keys(m.krs);
-    } else if constexpr (KM == KEYS_M0) {
+    } else if constexpr (KMODE == KEYS_M0) {
       word_keys(m.krs);
-    } else if (key_is_m3(m, fm)) {  // one chunk in flight: a wave-uniform branch
+    } else if (key_is_m3(m)) {  // one chunk in flight: a wave-uniform branch
       dma_keys(m.krs);
     } else {
       word_keys(m.krs);
@@ -608,8 +558,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   };
 
   // ---- registers -> an LDS stage buffer: value codes in padded rows, scales as loaded ([32][G] fp16) ----
-  auto stage_chunk = [&](const auto& R, uint32_t* lds, auto fm) __attribute__((always_inline)) {
-    constexpr int KM = decltype(fm)::value ? KEYS_M0 : KMODE;
+  auto stage_chunk = [&](const auto& R, uint32_t* lds) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k) {
       const int e = lane + 64 * k;
@@ -638,7 +587,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
         if constexpr (VAFF) put(lds + Cfg::VBS, R.vb[k], e, VG);
       }
     }
-    if constexpr (KM != KEYS_M3) {
+    if constexpr (KMODE != KEYS_M3) {
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
         const int e = lane + 64 * k;
@@ -651,19 +600,16 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   };
 
   // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
-  auto score_chunk = [&](const PageMeta& m, const auto& R, const uint32_t* lds, auto kbi, float* Ls,
-                         auto fm) __attribute__((always_inline)) {
-    constexpr bool M0O = decltype(fm)::value;
-    constexpr int KM = M0O ? KEYS_M0 : KMODE;
-    constexpr bool ROWS = kRowRegs && !M0O, DMAK = kDmaK && !M0O;
+  auto score_chunk = [&](const PageMeta& m, const auto& R, const uint32_t* lds, auto kbi,
+                         float* Ls) __attribute__((always_inline)) {
     const uint32_t* kl = kbuf(kbi);
     // MFMA results are read a few instructions after issue only at the very
     // end: the M3 paths keep four independent accumulation chains (token
     // tile hh x high / residual query part), the M0 path scales group g - 1
     // while the MFMAs of group g run
-    if (key_is_m3(m, fm)) {
-      if constexpr (DMAK || ROWS) {
-        const uint32_t l3 = KMODE == KEYS_M3 || ROWS ? 0u : fresh_lane();
+    if (key_is_m3(m)) {
+      if constexpr (kDmaK) {
+        const uint32_t l3 = KMODE == KEYS_M3 ? 0u : fresh_lane();
         f32x4 dh[2], dl[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) dh[hh] = dl[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -674,9 +620,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
           for (int hh = 0; hh < 2; ++hh) {
             // channels (0, 1), (2, 3), (4, 5), (6, 7) of the lane's 8
             u32x4 x;
-            if constexpr (ROWS)
-              x = R.kr[hh][g];
-            else if constexpr (KMODE == KEYS_M3)
+            if constexpr (KMODE == KEYS_M3)
               x = *reinterpret_cast<const u32x4*>(kl + krd[hh][g % 4] + 64 * (g / 4));
             else
               x = *reinterpret_cast<const u32x4*>(kl + krd_off(l3, hh, g % 4) + 64 * (g / 4));
@@ -699,7 +643,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
 #pragma unroll
           for (int i = 0; i < 4; ++i) Ls[4 * hh + i] = dh[hh][i] + dl[hh][i];
       }
-    } else if constexpr (KM != KEYS_M3) {  // M0 4- or 8-bit, group 32: scale and bias per group in fp32
+    } else if constexpr (KMODE != KEYS_M3) {  // M0 4- or 8-bit, group 32: scale and bias per group in fp32
       // affine: codes n, bias b; symmetric: codes n - (2^(KBITS-1) - 1), no
       // bias (bf = 0 zeroes the bias words, which then alias the scales)
       const bool k_affine = KAFF && m.kfmt == DC_FMT_M0_AFFINE;
@@ -786,13 +730,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             if constexpr (KBITS == 4) {
-              uint32_t w;
-              if constexpr (ROWS) {
-                const u32x4 x = R.kr[hh][g];
-                w = hh == 1 && last_row ? x.w : x.x;
-              } else {
-                w = R.kw[hh][g];
-              }
+              const uint32_t w = R.kw[hh][g];
               // nibble i of the word is channel i; channels i and i + 4 sit 16
               // bits apart, so one mask and the fp16 magic 0x6400 give the pair
               // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
@@ -807,15 +745,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
               // bytes (2j, 2j + 1) under the magic's 0x64 bytes, giving the
               // pair (1024 + n_2j, 1024 + n_2j+1), and one packed add makes
               // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
-              uint32_t wa, wb;
-              if constexpr (ROWS) {
-                const u32x4 x = R.kr[hh][g];
-                wa = hh == 1 && last_row ? x.z : x.x;
-                wb = hh == 1 && last_row ? x.w : x.y;
-              } else {
-                wa = R.kw[hh][2 * g];
-                wb = R.kw[hh][2 * g + 1];
-              }
+              const uint32_t wa = R.kw[hh][2 * g], wb = R.kw[hh][2 * g + 1];
               ka[hh].u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
               ka[hh].u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
               ka[hh].u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
@@ -896,10 +826,9 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   // same overflow margin: weight x scale x 16 reaches fp16's maximum only
   // for 8-bit scales above 1023).  The epilogue divides by kVS.
   constexpr float kVS = VBITS == 8 ? 16.f : 1.f;
-  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa, auto fm) __attribute__((always_inline)) {
-    constexpr bool VM3E = VM3 && !decltype(fm)::value;
+  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa) __attribute__((always_inline)) {
     bool v_m0 = true;
-    if constexpr (VM3E) v_m0 = is_m0(m.vfmt);
+    if constexpr (VM3) v_m0 = is_m0(m.vfmt);
     if (v_m0) {
       const bool v_affine = VAFF && m.vfmt == DC_FMT_M0_AFFINE;
       const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
@@ -996,7 +925,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
           }
         }
       }
-    } else if constexpr (VM3E) {  // M3 fp16 values (the exact recent window): rows staged in vbuf
+    } else if constexpr (VM3) {  // M3 fp16 values (the exact recent window): rows staged in vbuf
       Frag fa_hi, fa_res;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
@@ -1143,80 +1072,66 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       return m;
     };
 
-    auto run = [&](auto fm) __attribute__((always_inline)) {
-      using R_t = ChunkRegs<HD, VGS, VBITS, (decltype(fm)::value ? int(KEYS_M0) : KMODE), KBITS,
-                            (kRowRegs && !decltype(fm)::value)>;
-      if constexpr (kPipe) {
-        // chunk j is mixed from stage buffer j % 2 while chunk j + 1 is staged
-        // into the other buffer and scored, and the loads of chunk j + 2 fly
-        // into the register set chunk j + 1 came in; past the last chunk the
-        // loads go to an empty resource (no memory traffic)
-        uint32_t* const buf0 = lds_all;
-        uint32_t* const buf1 = lds_all + Cfg::STAGE;
-        R_t RA, RB;
-        PageMeta cur = chunk_meta(0);
-        PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
-        load_chunk(cur, RA, KB0{}, fm);
-        load_chunk(nxt, RB, KB1{}, fm);
-        prep_queries();
-        float Ls[8], pa[8];
-        stage_chunk(RA, buf0, fm);
-        score_chunk(cur, RA, buf0, KB0{}, Ls, fm);
-        softmax_chunk(cur, Ls, pa);
-        int j = 0;
-        // chunk j: values in stage buffer bm (keys in km, already scored);
-        // chunk j + 1: registers X, keys in ks; chunk j + 2 loads into Y, km
-        auto step = [&](R_t& X, R_t& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) __attribute__((always_inline)) -> bool {
-          if (j + 1 >= total) {  // last chunk: mix only
-            mix_chunk(cur, bm, pa, fm);
-            return false;
-          }
-          const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : no_chunk(nxt);
-          load_chunk(n2, Y, km, fm);
-          float Ln[8];
-          stage_chunk(X, bs, fm);
-          score_chunk(nxt, X, bs, ks, Ln, fm);
-          mix_chunk(cur, bm, pa, fm);
-          softmax_chunk(nxt, Ln, pa);
-          cur = nxt;
-          nxt = n2;
-          ++j;
-          return true;
-        };
-        while (step(RB, RA, buf0, buf1, KB0{}, KB1{}) && step(RA, RB, buf1, buf0, KB1{}, KB0{})) {
+    using R_t = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS>;
+    if constexpr (kPipe) {
+      // chunk j is mixed from stage buffer j % 2 while chunk j + 1 is staged
+      // into the other buffer and scored, and the loads of chunk j + 2 fly
+      // into the register set chunk j + 1 came in; past the last chunk the
+      // loads go to an empty resource (no memory traffic)
+      uint32_t* const buf0 = lds_all;
+      uint32_t* const buf1 = lds_all + Cfg::STAGE;
+      R_t RA, RB;
+      PageMeta cur = chunk_meta(0);
+      PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
+      load_chunk(cur, RA, KB0{});
+      load_chunk(nxt, RB, KB1{});
+      prep_queries();
+      float Ls[8], pa[8];
+      stage_chunk(RA, buf0);
+      score_chunk(cur, RA, buf0, KB0{}, Ls);
+      softmax_chunk(cur, Ls, pa);
+      int j = 0;
+      // chunk j: values in stage buffer bm (keys in km, already scored);
+      // chunk j + 1: registers X, keys in ks; chunk j + 2 loads into Y, km
+      auto step = [&](R_t& X, R_t& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) __attribute__((always_inline)) -> bool {
+        if (j + 1 >= total) {  // last chunk: mix only
+          mix_chunk(cur, bm, pa);
+          return false;
         }
-      } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
-        // (M3 value rows go to vbuf once the previous chunk's mix has read it)
-        constexpr bool VM3E = VM3 && !decltype(fm)::value;
-        R_t R;
-        PageMeta cur = chunk_meta(0);
-        load_chunk(cur, R, KB0{}, fm);
-        if constexpr (VM3E)
-          if (!is_m0(cur.vfmt)) load_value_rows(cur);
-        prep_queries();
-        for (int j = 0; j < total; ++j) {
-          const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
-          float Ls[8], pa[8];
-          stage_chunk(R, lds_all, fm);
-          score_chunk(cur, R, lds_all, KB0{}, Ls, fm);
-          load_chunk(nm, R, KB0{}, fm);
-          softmax_chunk(cur, Ls, pa);
-          mix_chunk(cur, lds_all, pa, fm);
-          if constexpr (VM3E)
-            if (j + 1 < total && !is_m0(nm.vfmt)) load_value_rows(nm);
-          cur = nm;
-        }
+        const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : no_chunk(nxt);
+        load_chunk(n2, Y, km);
+        float Ln[8];
+        stage_chunk(X, bs);
+        score_chunk(nxt, X, bs, ks, Ln);
+        mix_chunk(cur, bm, pa);
+        softmax_chunk(nxt, Ln, pa);
+        cur = nxt;
+        nxt = n2;
+        ++j;
+        return true;
+      };
+      while (step(RB, RA, buf0, buf1, KB0{}, KB1{}) && step(RA, RB, buf1, buf0, KB1{}, KB0{})) {
       }
-    };
-    if constexpr (kTwoLoops) {
-      // the batch's valid pages all hold M0 keys and values: the M0 loop
-      const uint64_t other = __ballot(T > 0 && !(km0 && vm0));
-      if (other == 0)
-        run(FM_M0{});
-      else
-        run(FM_ANY{});
-    } else {
-      run(FM_ANY{});
+    } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
+      // (M3 value rows go to vbuf once the previous chunk's mix has read it)
+      R_t R;
+      PageMeta cur = chunk_meta(0);
+      load_chunk(cur, R, KB0{});
+      if constexpr (VM3)
+        if (!is_m0(cur.vfmt)) load_value_rows(cur);
+      prep_queries();
+      for (int j = 0; j < total; ++j) {
+        const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
+        float Ls[8], pa[8];
+        stage_chunk(R, lds_all);
+        score_chunk(cur, R, lds_all, KB0{}, Ls);
+        load_chunk(nm, R, KB0{});
+        softmax_chunk(cur, Ls, pa);
+        mix_chunk(cur, lds_all, pa);
+        if constexpr (VM3)
+          if (j + 1 < total && !is_m0(nm.vfmt)) load_value_rows(nm);
+        cur = nm;
+      }
     }
   }
 
