@@ -350,6 +350,16 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   auto prep_queries = [&]() __attribute__((always_inline)) {
     if (q_ready) return;
     q_ready = true;
+    // Pipelined instances: the raw queries pass through an empty asm here,
+    // so their conversion stays where it is called.  Without it the
+    // compiler hoists the conversion (loop-invariant) above the page walk,
+    // and the layout then waits for the query loads before the first
+    // chunk's loads can issue (C3: 32.65 -> 32.15 us per launch).  The
+    // unpipelined instances measured 0.4-1 us slower with it.
+    if constexpr (kPipe) {
+#pragma unroll
+      for (int i = 0; i < 2 * KG; ++i) asm volatile("" : "+v"(qraw[i]));
+    }
     float qv[KG][8];
     if (q_f32) {
 #pragma unroll
