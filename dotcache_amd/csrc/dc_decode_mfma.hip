@@ -989,6 +989,85 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   // loads would cost registers it does not have
   if constexpr (HD > 128) prep_queries();
 
+  // Lane i: everything about page base + i of a batch whose descriptors
+  // are in (k0, k1, v0, v1), vector work instead of per-page scalar work:
+  // token count, formats, blob sizes, scale / bias offsets.  Blob layout
+  // (dc_common.h blob_layout) of the formats this kernel accepts, from its
+  // fixed geometry: keys M3 fp16 or M0 KBITS-bit group 32, values M3 fp16
+  // or M0 VBITS-bit group VGS, capacity CAP.  (The early first chunk below
+  // uses these helpers; the batch walk computes the same fields inline,
+  // which the unpipelined instances compile to faster code.)
+  struct PageFields {
+    uint32_t ktot, vtot, info, koffs, voffs;
+    int T;
+  };
+  auto page_fields = [&](int nb) __attribute__((always_inline)) -> PageFields {
+    const int kf = int(k1 >> 16) & 0xff, vf = int(v1 >> 16) & 0xff;
+    const uint32_t cap = uint32_t(CAP), m3_bytes = cap * HD * 2;
+    const uint32_t kpay = uint32_t(KG) * cap * KBLK, ksb = (cap * KG * 2 + 15) & ~15u;
+    const uint32_t vpay = uint32_t(VG) * cap * W * 4, vsb = (cap * VG * 2 + 15) & ~15u;
+    const bool km0 = is_m0(kf), vm0 = is_m0(vf), kaff = kf == DC_FMT_M0_AFFINE, vaff = vf == DC_FMT_M0_AFFINE;
+    const uint32_t ksc = km0 ? kpay : 0u, kbs = kaff ? kpay + ksb : ksc;
+    const uint32_t vsc = vm0 ? vpay : 0u, vbs = vaff ? vpay + vsb : vsc;
+    PageFields f;
+    f.ktot = km0 ? kpay + ksb + (kaff ? ksb : 0u) : m3_bytes;
+    f.vtot = vm0 ? vpay + vsb + (vaff ? vsb : 0u) : m3_bytes;
+    int T = min(int(k1 & 0xffff), int(v1 & 0xffff));
+    T = min(T, CAP);
+    // (bitwise, not short-circuit: no branch)
+    const bool bad = !ok | (lane >= nb) | ((uint64_t(k0) << 8) + f.ktot > uint64_t(a.kpool.arena_bytes)) |
+                     ((uint64_t(v0) << 8) + f.vtot > uint64_t(a.vpool.arena_bytes));
+    f.T = bad ? 0 : T;
+    f.info = uint32_t(f.T) | (uint32_t(kf) << 16) | (uint32_t(vf) << 24);
+    f.koffs = ksc | (kbs << 16);  // offsets < 64 KiB for M0 pages
+    f.voffs = vsc | (vbs << 16);
+    return f;
+  };
+  // the chunk of lane i's page that starts at token c0
+  auto lane_meta = [&](const PageFields& f, int i, int c0) __attribute__((always_inline)) -> PageMeta {
+    PageMeta m;
+    // blob pointers stay derived from the arena arguments (global memory)
+    const uint8_t* kp =
+        reinterpret_cast<const uint8_t*>(a.kpool.arena) + (uint64_t(__builtin_amdgcn_readlane(k0, i)) << 8);
+    m.vp = reinterpret_cast<const uint8_t*>(a.vpool.arena) + (uint64_t(__builtin_amdgcn_readlane(v0, i)) << 8);
+    m.krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(kp), 0, int(__builtin_amdgcn_readlane(f.ktot, i)),
+                                              0x00020000);
+    m.vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.vp), 0,
+                                              int(__builtin_amdgcn_readlane(f.vtot, i)), 0x00020000);
+    const uint32_t inf = __builtin_amdgcn_readlane(f.info, i);
+    m.T = int(inf & 0xffff);
+    m.kfmt = int(inf >> 16) & 0xff;
+    m.vfmt = int(inf >> 24);
+    const uint32_t ko = __builtin_amdgcn_readlane(f.koffs, i), vo = __builtin_amdgcn_readlane(f.voffs, i);
+    m.ksc = ko & 0xffff;
+    m.kbs = ko >> 16;
+    m.vsc = vo & 0xffff;
+    m.vbs = vo >> 16;
+    m.c0 = c0;
+    return m;
+  };
+  using R_t = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS>;
+  R_t RA, RB;  // the pipeline's register sets
+  // Pipelined instances with DMA keys issue the item's first chunk straight
+  // from page 0's descriptors, before the batch layout (its prefix sum, the
+  // chunk count and the loop set-up), when page 0 holds that chunk.  The
+  // layout then runs while the loads fly (C3: 32.36 -> 31.87 us per
+  // launch; C2, M0 keys at head_dim 64 and two chunks per item, measured
+  // 0.08 us slower with it).
+  bool early = false;
+  if constexpr (kPipe && kDmaK) {
+    if (np > 0) {
+      // (the item's chunks: from chunk cb of its first page to, with ce > 0,
+      // chunk ce - 1 of its last page)
+      const int cpp = CAP >> 5;
+      const int cb = min(it.chunk_begin, cpp - 1), ce = min(it.chunk_end, cpp);
+      const PageFields f = page_fields(np < 64 ? np : 64);
+      const int nch0 = (__builtin_amdgcn_readlane(f.T, 0) + 31) >> 5;
+      early = cb < (np == 1 && ce > 0 ? min(nch0, ce) : nch0);
+      if (early) load_chunk(lane_meta(f, 0, cb * 32), RA, KB0{});
+    }
+  }
+
   // ---- walk the pages: metadata 64 pages at a time, chunks pipelined ----
   for (int base = 0; base < np; base += 64) {
     const int nb = np - base < 64 ? np - base : 64;
@@ -996,12 +1075,6 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       load_ids(base);
       load_descs();
     }
-    // lane i: everything about page base + i, once for the batch (vector
-    // work instead of per-page scalar work): token count, formats, blob
-    // sizes, scale / bias offsets, and its end chunk index in the batch
-    // blob layout (dc_common.h blob_layout) of the formats this kernel
-    // accepts, from its fixed geometry: keys M3 fp16 or M0 KBITS-bit group 32,
-    // values M3 fp16 or M0 VBITS-bit group VGS, capacity CAP
     const int kf = int(k1 >> 16) & 0xff, vf = int(v1 >> 16) & 0xff;
     const uint32_t cap = uint32_t(CAP), m3_bytes = cap * HD * 2;
     const uint32_t kpay = uint32_t(KG) * cap * KBLK, ksb = (cap * KG * 2 + 15) & ~15u;
@@ -1082,7 +1155,6 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       return m;
     };
 
-    using R_t = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS>;
     if constexpr (kPipe) {
       // chunk j is mixed from stage buffer j % 2 while chunk j + 1 is staged
       // into the other buffer and scored, and the loads of chunk j + 2 fly
@@ -1090,14 +1162,20 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       // loads go to an empty resource (no memory traffic)
       uint32_t* const buf0 = lds_all;
       uint32_t* const buf1 = lds_all + Cfg::STAGE;
-      R_t RA, RB;
       PageMeta cur = chunk_meta(0);
       PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
-      load_chunk(cur, RA, KB0{});
+      if (!(early && base == 0)) load_chunk(cur, RA, KB0{});  // (early: the same chunk, already issued)
       load_chunk(nxt, RB, KB1{});
       prep_queries();
       float Ls[8], pa[8];
       stage_chunk(RA, buf0);
+      // A chunk's key rows (LDS filled by DMA) are read only after its
+      // stage, whose waits for the chunk's register loads also cover the
+      // key DMA issued before them (vector memory loads complete in order).
+      // The compiler's own wait for the DMA went missing on a path into
+      // this block once the first chunk could be issued before the loop,
+      // and the reads it hoisted above the stage then saw stale rows.
+      if constexpr (kDmaK) asm volatile("" ::: "memory");
       score_chunk(cur, RA, buf0, KB0{}, Ls);
       softmax_chunk(cur, Ls, pa);
       int j = 0;
@@ -1112,6 +1190,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
         load_chunk(n2, Y, km);
         float Ln[8];
         stage_chunk(X, bs);
+        if constexpr (kDmaK) asm volatile("" ::: "memory");  // (as for the first chunk)
         score_chunk(nxt, X, bs, ks, Ln);
         mix_chunk(cur, bm, pa);
         softmax_chunk(nxt, Ln, pa);
