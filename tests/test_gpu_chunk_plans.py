@@ -171,6 +171,45 @@ def test_single_page_items_and_empty_items():
     assert err < KERNEL_TOL, f"max-abs error {err}"
 
 
+@pytest.mark.parametrize("records", [False, True])
+def test_first_chunk_cases_on_the_dma_key_instance(records):
+    """The config 3 instance (M3 keys by DMA, pipelined) issues an item's
+    first chunk before its batch layout when the item's first page holds
+    it.  Items here start inside a page (chunk 1 of 2), end inside one,
+    start on a partial page's missing chunk (no valid tokens: an empty
+    partial) or on an empty page, beside a whole-sequence item; through
+    the tables and through page records."""
+    import torch
+
+    from dotcache_amd.decode import DecodePlan, decode_paged, gather_records, set_decode_path
+
+    set_decode_path("mfma")
+    rng = np.random.default_rng(91)
+    hd, Q, tpp, cpp = 128, 7, 64, 2
+    # sequence 0: 4 pages, the last with 20 tokens (chunk 1 of it empty);
+    # sequence 1: an empty page, then 2 full pages
+    case = _case(rng, [tpp * 3 + 20, tpp * 2], hd, Q, tpp, dict(mode="M3"), dict(bits=4, scheme="symmetric"), 32,
+                 empty_at=(1, 0))
+    items = [
+        [0, 0, 0, 1, 0, 0, 1, 0],    # page 0, chunk 0
+        [0, 0, 0, 1, 1, 1, 0, 0],    # page 0, chunk 1
+        [0, 0, 1, 3, 2, 0, 1, 0],    # page 1 to page 2 chunk 0
+        [0, 0, 2, 4, 3, 1, 1, 0],    # page 2 chunk 1 to page 3 chunk 0 (its only valid chunk)
+        [0, 0, 3, 4, 4, 1, 0, 0],    # page 3 chunk 1: no valid tokens, an empty partial
+        [1, 0, 0, 3, -1, 0, 0, 0],   # sequence 1 whole, starting on its empty page
+    ]
+    it = np.asarray(items, np.int32)
+    ms = np.asarray([[0, 0, 0, 5]], np.int32)
+    plan = DecodePlan(torch.from_numpy(it.ravel().view(np.uint8).copy()).cuda(),
+                      torch.from_numpy(ms.ravel().view(np.uint8).copy()).cuda(), len(it), 1, 5, 0, it, ms,
+                      chunks_per_page=cpp)
+    args = (case["kpool"], case["kt"], case["vt"], case["counts"])
+    rec = gather_records(*args, plan, v_pool=case["vpool"]) if records else None
+    got = decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"], records=rec).cpu().numpy()[:, 0]
+    err = float(np.max(np.abs(got - case["want"])))
+    assert err < KERNEL_TOL, f"records {records}: max-abs error {err}"
+
+
 @pytest.mark.parametrize("kfmt,vfmt,vgs,hd,Q,tpp", CASES[:3])
 def test_page_records_give_the_same_outputs(kfmt, vfmt, vgs, hd, Q, tpp):
     """Decode with page records (every item's descriptors gathered ahead)
