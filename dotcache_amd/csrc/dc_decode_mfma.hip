@@ -14,6 +14,8 @@
 // Prologue: the item, then its pages' table entries, then their
 // descriptors -- or, with page records (dc_gather_page_records), the item
 // and its pages' descriptors in one round, indexed by the workgroup id.
+// Pipelined instances with DMA keys then issue the item's first chunk
+// straight from page 0's descriptors, before the batch layout.
 //
 // Pipeline (one wave per SIMD, head_dim <= 128, one key format, no M3
 // values): while chunk j is mixed, chunk j + 1 is staged and scored and
