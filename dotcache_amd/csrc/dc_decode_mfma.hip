@@ -509,7 +509,9 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   }
   const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
-  auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi) __attribute__((always_inline)) {
+  // part 0: the whole chunk; 1: value pieces and all scales / biases; 2: key codes or rows
+  auto load_part = [&](const PageMeta& m, auto& R, auto kbi, auto part) __attribute__((always_inline)) {
+    constexpr int P = decltype(part)::value;
     const int c0 = m.c0;
     auto dma_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
       const uint32_t l = KMODE == KEYS_M3 ? 0u : fresh_lane();
@@ -524,6 +526,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       }
     };
     auto word_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
+      if constexpr (P != 1)
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
@@ -541,6 +544,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       // the scale / bias offsets are wave-uniform; readfirstlane says so, or
       // the compiler wraps each of these loads in a per-value loop
       const int ksc = __builtin_amdgcn_readfirstlane(int(m.ksc)), kbs = __builtin_amdgcn_readfirstlane(int(m.kbs));
+      if constexpr (P != 2)
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
         R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(ksoff), ksc + c0 * KG * 2 + 256 * k, kNT);
@@ -549,14 +553,15 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       }
     };
     if constexpr (KMODE == KEYS_M3) {
-      dma_keys(m.krs);
+      if constexpr (P != 1) dma_keys(m.krs);
     } else if constexpr (KMODE == KEYS_M0) {
       word_keys(m.krs);
     } else if (key_is_m3(m)) {  // one chunk in flight: a wave-uniform branch
-      dma_keys(m.krs);
+      if constexpr (P != 1) dma_keys(m.krs);
     } else {
       word_keys(m.krs);
     }
+    if constexpr (P == 2) return;
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k)
       R.vr[k] = __builtin_amdgcn_raw_buffer_load_b128(m.vrs, int(voff[k]), c0 * W * 4, kNT);
@@ -567,6 +572,13 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       if constexpr (VAFF)
         R.vb[k] = __builtin_amdgcn_raw_buffer_load_b32(m.vrs, int(vsoff), vbs + c0 * VG * 2 + 256 * k, kNT);
     }
+  };
+  constexpr bool kSplitReload = !kPipe && waves_per_simd<HD, KMODE, KBITS, VBITS, NQB>() == 1;
+  using LP0 = std::integral_constant<int, 0>;
+  using LP1 = std::integral_constant<int, 1>;
+  using LP2 = std::integral_constant<int, 2>;
+  auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi) __attribute__((always_inline)) {
+    load_part(m, R, kbi, LP0{});
   };
 
   // ---- registers -> an LDS stage buffer: value codes in padded rows, scales as loaded ([32][G] fp16) ----
@@ -1215,8 +1227,14 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
         const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
         float Ls[8], pa[8];
         stage_chunk(R, lds_all);
+        // At one wave per SIMD the value pieces and scales of chunk j + 1
+        // go out as soon as this chunk is staged, and its key codes / rows
+        // once this chunk is scored (C5: 164.4 -> 162.6 us per launch); with
+        // two waves per SIMD the other wave covers the wait, and the early
+        // half measured slower (C4: 40.7 -> 41.4 us).
+        if constexpr (kSplitReload) load_part(nm, R, KB0{}, LP1{});
         score_chunk(cur, R, lds_all, KB0{}, Ls);
-        load_chunk(nm, R, KB0{});
+        load_part(nm, R, KB0{}, std::integral_constant<int, kSplitReload ? 2 : 0>{});
         softmax_chunk(cur, Ls, pa);
         mix_chunk(cur, lds_all, pa);
         if constexpr (VM3)
