@@ -509,7 +509,8 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   }
   const uint32_t vsoff = uint32_t(lane % Cfg::VSW) * 4, ksoff = uint32_t(lane % Cfg::KSW) * 4;
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
-  // part 0: the whole chunk; 1: value pieces and all scales / biases; 2: key codes or rows
+  // part 0: the whole chunk; 1: value pieces and all scales / biases;
+  // 2: key codes or rows; 3: M0 key codes only; 4: M3 key rows only
   auto load_part = [&](const PageMeta& m, auto& R, auto kbi, auto part) __attribute__((always_inline)) {
     constexpr int P = decltype(part)::value;
     const int c0 = m.c0;
@@ -526,7 +527,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       }
     };
     auto word_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
-      if constexpr (P != 1)
+      if constexpr (P == 0 || P == 2 || P == 3)
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
@@ -544,7 +545,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       // the scale / bias offsets are wave-uniform; readfirstlane says so, or
       // the compiler wraps each of these loads in a per-value loop
       const int ksc = __builtin_amdgcn_readfirstlane(int(m.ksc)), kbs = __builtin_amdgcn_readfirstlane(int(m.kbs));
-      if constexpr (P != 2)
+      if constexpr (P == 0 || P == 1)
 #pragma unroll
       for (int k = 0; k < Cfg::NKS; ++k) {
         R.ks[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(ksoff), ksc + c0 * KG * 2 + 256 * k, kNT);
@@ -553,15 +554,15 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       }
     };
     if constexpr (KMODE == KEYS_M3) {
-      if constexpr (P != 1) dma_keys(m.krs);
+      if constexpr (P == 0 || P == 2 || P == 4) dma_keys(m.krs);
     } else if constexpr (KMODE == KEYS_M0) {
-      word_keys(m.krs);
+      if constexpr (P != 4) word_keys(m.krs);
     } else if (key_is_m3(m)) {  // one chunk in flight: a wave-uniform branch
-      if constexpr (P != 1) dma_keys(m.krs);
+      if constexpr (P == 0 || P == 2 || P == 4) dma_keys(m.krs);
     } else {
-      word_keys(m.krs);
+      if constexpr (P != 4) word_keys(m.krs);
     }
-    if constexpr (P == 2) return;
+    if constexpr (P >= 2) return;
 #pragma unroll
     for (int k = 0; k < Cfg::NVP; ++k)
       R.vr[k] = __builtin_amdgcn_raw_buffer_load_b128(m.vrs, int(voff[k]), c0 * W * 4, kNT);
@@ -577,6 +578,8 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   using LP0 = std::integral_constant<int, 0>;
   using LP1 = std::integral_constant<int, 1>;
   using LP2 = std::integral_constant<int, 2>;
+  using LP3 = std::integral_constant<int, 3>;
+  using LP4 = std::integral_constant<int, 4>;
   auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi) __attribute__((always_inline)) {
     load_part(m, R, kbi, LP0{});
   };
@@ -1217,7 +1220,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       }
     } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
       // (M3 value rows go to vbuf once the previous chunk's mix has read it)
-      R_t R;
+      R_t R, RN;
       PageMeta cur = chunk_meta(0);
       load_chunk(cur, R, KB0{});
       if constexpr (VM3)
@@ -1227,18 +1230,28 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
         const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
         float Ls[8], pa[8];
         stage_chunk(R, lds_all);
-        // At one wave per SIMD the value pieces and scales of chunk j + 1
-        // go out as soon as this chunk is staged, and its key codes / rows
-        // once this chunk is scored (C5: 164.4 -> 162.6 us per launch); with
-        // two waves per SIMD the other wave covers the wait, and the early
-        // half measured slower (C4: 40.7 -> 41.4 us).
-        if constexpr (kSplitReload) load_part(nm, R, KB0{}, LP1{});
+        // At one wave per SIMD the value pieces, scales and M0 key codes of
+        // chunk j + 1 go out as soon as this chunk is staged (the codes into
+        // a second set, copied over after the mix), and M3 key rows once
+        // this chunk is scored, its key buffer then being free (C5: 164.4 ->
+        // 162.6 us per launch for the values and scales, -> 161.6 us with
+        // the codes); with two waves per SIMD the other wave covers the
+        // wait, and the early values measured slower (C4: 40.7 -> 41.4 us).
+        if constexpr (kSplitReload) {
+          load_part(nm, R, KB0{}, LP1{});
+          if constexpr (KMODE != KEYS_M3) load_part(nm, RN, KB0{}, LP3{});  // (an M3 key page loads none)
+        }
         score_chunk(cur, R, lds_all, KB0{}, Ls);
-        load_part(nm, R, KB0{}, std::integral_constant<int, kSplitReload ? 2 : 0>{});
+        load_part(nm, R, KB0{}, std::integral_constant<int, kSplitReload ? 4 : 0>{});
         softmax_chunk(cur, Ls, pa);
         mix_chunk(cur, lds_all, pa);
         if constexpr (VM3)
           if (j + 1 < total && !is_m0(nm.vfmt)) load_value_rows(nm);
+        if constexpr (kSplitReload && KMODE != KEYS_M3)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int i = 0; i < Cfg::KG * (KBITS / 4); ++i) R.kw[hh][i] = RN.kw[hh][i];
         cur = nm;
       }
     }
