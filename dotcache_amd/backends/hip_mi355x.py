@@ -239,8 +239,10 @@ def _queries_tensor(q, hd: int, device):
     return t.contiguous()
 
 
-def _score_tensor(queries, pool: DevicePagePool, ids: np.ndarray):
-    """logits [n_queries, total_tokens] on the device."""
+def _score_tensor(queries, pool: DevicePagePool, ids: np.ndarray, score=None):
+    """logits [n_queries, total_tokens] on the device.  With ``score`` (a
+    bool mask over the pages), only those pages are scored; the columns of
+    the others are left unwritten."""
     torch = _torch()
     dev = pool.device
     tok = pool.tokens_of(ids)
@@ -249,12 +251,14 @@ def _score_tensor(queries, pool: DevicePagePool, ids: np.ndarray):
     total = int(offsets[-1])
     q = _queries_tensor(queries, pool.geometry.head_dim, dev)
     logits = torch.empty((q.shape[0], total), dtype=torch.float32, device=dev)
-    ids_d = torch.from_numpy(ids).to(dev)
-    off_d = torch.from_numpy(offsets).to(dev)
-    st = _lib.lib().dc_score_pages(pool.c_pool(), C.c_void_p(ids_d.data_ptr()), C.c_void_p(off_d.data_ptr()), ids.size,
-                                   C.c_void_p(q.data_ptr()), q.shape[0], C.c_void_p(logits.data_ptr()), total,
-                                   C.c_void_p(current_stream_ptr()))
-    _lib.check(st, "dc_score_pages")
+    sel_ids, sel_off = (ids, offsets) if score is None else (ids[score], offsets[:-1][score])
+    if sel_ids.size:
+        ids_d = torch.from_numpy(np.ascontiguousarray(sel_ids)).to(dev)
+        off_d = torch.from_numpy(np.ascontiguousarray(sel_off)).to(dev)
+        st = _lib.lib().dc_score_pages(pool.c_pool(), C.c_void_p(ids_d.data_ptr()), C.c_void_p(off_d.data_ptr()),
+                                       sel_ids.size, C.c_void_p(q.data_ptr()), q.shape[0],
+                                       C.c_void_p(logits.data_ptr()), total, C.c_void_p(current_stream_ptr()))
+        _lib.check(st, "dc_score_pages")
     return logits, offsets
 
 
@@ -341,23 +345,34 @@ def _pair_pools(key_pages, value_pages, trace):
 
 def decode_multi_query_step_hip_tensor(query_slices, key_pages, value_pages, *, precomputed_page_logits=None,
                                        trace: ExecutionTrace | None = None):
-    """(logits [Q, T], weights [Q, T], output [Q, head_dim]) as device tensors."""
+    """(logits [Q, T], weights [Q, T], output [Q, head_dim]) as device tensors.
+
+    ``precomputed_page_logits[i]``, when not None, is used as page i's logits
+    and page i's key bytes are not read (reference
+    ``decode_step_with_page_logits``, dotcache/attention_runtime.py:298-303,
+    and its device path dotcache/backends/torch_mps.py:2690-2700); the trace
+    counts the key pages scored and every value page."""
     torch = _torch()
     kpool, vpool, kid, vid, prepared = _pair_pools(key_pages, value_pages, trace)
-    _record_reads(trace, prepared, "decode_multi_query_step")
-    logits, offsets = _score_tensor(query_slices, kpool, kid)
+    kprep, vprep = prepared[:kid.size], prepared[kid.size:]
+    cached = [None] * kid.size
     if precomputed_page_logits is not None:
         if len(precomputed_page_logits) != kid.size:
             raise ValueError("precomputed_page_logits must align with key_pages")
-        for i, cached in enumerate(precomputed_page_logits):
-            if cached is None:
-                continue
-            c = torch.as_tensor(np.asarray(cached, dtype=np.float32) if not isinstance(cached, torch.Tensor) else cached,
-                                dtype=torch.float32, device=kpool.device)
-            n = int(offsets[i + 1] - offsets[i])
-            if c.numel() != n:
-                raise ValueError("precomputed page logits must have shape [token_count]")
-            logits[:, offsets[i]: offsets[i + 1]] = c.reshape(1, n)
+        cached = list(precomputed_page_logits)
+    score = np.asarray([c is None for c in cached], dtype=bool)
+    kread = [p for p, s in zip(kprep, score) if s]
+    _record_reads(trace, kread + list(vprep), "decode_multi_query_step")
+    logits, offsets = _score_tensor(query_slices, kpool, kid, score=None if score.all() else score)
+    for i, c in enumerate(cached):
+        if c is None:
+            continue
+        c = torch.as_tensor(np.asarray(c, dtype=np.float32) if not isinstance(c, torch.Tensor) else c,
+                            dtype=torch.float32, device=kpool.device)
+        n = int(offsets[i + 1] - offsets[i])
+        if c.numel() != n:
+            raise ValueError("precomputed page logits must have shape [token_count]")
+        logits[:, offsets[i]: offsets[i + 1]] = c.reshape(1, n)
     weights = logits.clone()
     _softmax_(weights)
     out = _mix_tensor(weights, vpool, vid)

@@ -277,9 +277,11 @@ class DeviceVllmPagedKVCache:
         order_t = torch.from_numpy(order).to(self.device)
         qg = (q if contiguous else q[:, order_t]).reshape(B, H, Hq // H, hd)
         seq_pages = n_blocks.astype(np.int32)
+        last_tokens = np.asarray([self._fill[lid][bt_host[b, n_blocks[b] - 1]] for b in range(B)], dtype=np.int32)
         plan = make_plan(seq_pages, H, device=self.device,
                          chunks_per_page=chunks_per_page(self.k_pool.geometry.page_capacity),
-                         target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H))
+                         target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H),
+                         last_page_tokens=last_tokens)
         need = workspace_bytes(plan, Hq // H, hd)
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.device)

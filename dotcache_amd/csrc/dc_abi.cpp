@@ -115,8 +115,9 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
   return DC_OK;
 }
 
-int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t chunks_per_page,
-                        const float* page_cost, int64_t cost_stride, int32_t target_items,
+int dc_plan_decode_fill(const int32_t* seq_pages, const int32_t* last_page_tokens, int32_t n_seqs,
+                        int32_t n_kv_heads, int32_t chunks_per_page, const float* page_cost, int64_t cost_stride,
+                        int32_t target_items,
                         int32_t min_chunks_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
                         dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials,
                         int32_t* largest_item) {
@@ -128,8 +129,17 @@ int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_h
     if (seq_pages[b] <= 0)
       return dc::fail(DC_EINVAL, "decode requires at least one page (sequence %d has %d)", b, seq_pages[b]);
     top = std::max(top, seq_pages[b]);
+    if (last_page_tokens && (last_page_tokens[b] <= 0 || last_page_tokens[b] > 32 * chunks_per_page))
+      return dc::fail(DC_EINVAL, "dc_plan_decode_fill: sequence %d's last page holds %d tokens (1 .. %d allowed)", b,
+                      last_page_tokens[b], 32 * chunks_per_page);
   }
   const int64_t cpp = chunks_per_page;
+  // chunks that hold tokens in each sequence's last page (all of them
+  // without last_page_tokens): a stream's chunks past its last token are
+  // not counted, so no cut falls among them and no item is empty
+  auto last_chunks = [&](int32_t b) -> int64_t {
+    return last_page_tokens ? std::min<int64_t>(cpp, (last_page_tokens[b] + 31) / 32) : cpp;
+  };
   if (int64_t(top) * cpp > INT32_MAX) return dc::fail(DC_EINVAL, "dc_plan_decode_fill: sequence too long");
   if (page_cost && cost_stride < top)
     return dc::fail(DC_EINVAL, "dc_plan_decode_fill: cost_stride %lld is below the longest sequence's %d pages",
@@ -149,7 +159,7 @@ int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_h
         w += c[p];
       }
     } else {
-      w = double(pages) * cpp;
+      w = double(pages - 1) * cpp + double(last_chunks(s / n_kv_heads));
     }
     total[s] = w;
   }
@@ -157,7 +167,10 @@ int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_h
   // stream with the largest mean item cost total / splits (compared as
   // products, ties to the longer stream, then the lower index)
   std::vector<int32_t> splits(S, 1);
-  auto chunks = [&](int32_t s) { return int64_t(seq_pages[s / n_kv_heads]) * cpp; };
+  auto chunks = [&](int32_t s) {
+    const int32_t b = s / n_kv_heads;
+    return int64_t(seq_pages[b] - 1) * cpp + last_chunks(b);
+  };
   auto before = [&](int32_t x, int32_t y) {  // true when x's items rank below y's
     const double lx = total[x] * splits[y], ly = total[y] * splits[x];
     if (lx != ly) return lx < ly;
@@ -190,8 +203,13 @@ int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_h
     cut[n] = len;
     if (page_cost && total[s] > 0.0 && n > 1) {
       const float* c = page_cost + int64_t(s) * cost_stride;
+      // a page's cost spread over its chunks (the last page's over the
+      // chunks that hold tokens)
+      const int64_t full = int64_t(seq_pages[b] - 1) * cpp;
+      const double last_n = double(len - full);
       prefix.assign(len + 1, 0.0);
-      for (int64_t u = 0; u < len; ++u) prefix[u + 1] = prefix[u] + double(c[u / cpp]) / double(cpp);
+      for (int64_t u = 0; u < len; ++u)
+        prefix[u + 1] = prefix[u] + double(c[u / cpp]) / (u < full ? double(cpp) : last_n);
       for (int32_t i = 1; i < n; ++i) {
         const double goal = total[s] * i / n * (1.0 + 1e-12);
         int64_t u = int64_t(std::upper_bound(prefix.begin(), prefix.end(), goal) - prefix.begin()) - 1;

@@ -1037,8 +1037,11 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
                      ((uint64_t(v0) << 8) + f.vtot > uint64_t(a.vpool.arena_bytes));
     f.T = bad ? 0 : T;
     f.info = uint32_t(f.T) | (uint32_t(kf) << 16) | (uint32_t(vf) << 24);
-    f.koffs = ksc | (kbs << 16);  // offsets < 64 KiB for M0 pages
-    f.voffs = vsc | (vbs << 16);
+    // offsets in 16-byte units (blob offsets are 16-byte aligned): an M0
+    // page at head_dim 256 and capacity 256 puts its 8-bit codes' scales at
+    // 64 KiB, past a 16-bit byte offset
+    f.koffs = (ksc >> 4) | ((kbs >> 4) << 16);
+    f.voffs = (vsc >> 4) | ((vbs >> 4) << 16);
     return f;
   };
   // the chunk of lane i's page that starts at token c0
@@ -1057,10 +1060,10 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
     m.kfmt = int(inf >> 16) & 0xff;
     m.vfmt = int(inf >> 24);
     const uint32_t ko = __builtin_amdgcn_readlane(f.koffs, i), vo = __builtin_amdgcn_readlane(f.voffs, i);
-    m.ksc = ko & 0xffff;
-    m.kbs = ko >> 16;
-    m.vsc = vo & 0xffff;
-    m.vbs = vo >> 16;
+    m.ksc = (ko & 0xffff) << 4;
+    m.kbs = (ko >> 16) << 4;
+    m.vsc = (vo & 0xffff) << 4;
+    m.vbs = (vo >> 16) << 4;
     m.c0 = c0;
     return m;
   };
@@ -1109,7 +1112,8 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
                      ((uint64_t(v0) << 8) + vtot > uint64_t(a.vpool.arena_bytes));
     if (bad) T = 0;
     const uint32_t info = uint32_t(T) | (uint32_t(kf) << 16) | (uint32_t(vf) << 24);
-    const uint32_t koffs = ksc | (kbs << 16), voffs = vsc | (vbs << 16);  // offsets < 64 KiB for M0 pages
+    // (16-byte units, as in page_fields)
+    const uint32_t koffs = (ksc >> 4) | ((kbs >> 4) << 16), voffs = (vsc >> 4) | ((vbs >> 4) << 16);
     const int nch = (T + 31) >> 5;  // <= 8 (capacity <= 256)
     // The item's chunks of page lane: [lo, hi).  It starts at chunk cb of
     // its first page (lane 0 of the first batch: `off` chunks skipped) and,
@@ -1165,10 +1169,10 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       m.kfmt = int(inf >> 16) & 0xff;
       m.vfmt = int(inf >> 24);
       const uint32_t ko = __builtin_amdgcn_readlane(koffs, i), vo = __builtin_amdgcn_readlane(voffs, i);
-      m.ksc = ko & 0xffff;
-      m.kbs = ko >> 16;
-      m.vsc = vo & 0xffff;
-      m.vbs = vo >> 16;
+      m.ksc = (ko & 0xffff) << 4;
+      m.kbs = (ko >> 16) << 4;
+      m.vsc = (vo & 0xffff) << 4;
+      m.vbs = (vo >> 16) << 4;
       m.c0 = fast ? ((j + off) & (cpp - 1)) * 32 : (j - __builtin_amdgcn_readlane(cbeg, i) + (i == 0 ? off : 0)) * 32;
       return m;
     };
@@ -1221,11 +1225,16 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       }
     } else {  // one register set and stage buffer: reload as soon as the chunk has consumed them
       // (M3 value rows go to vbuf once the previous chunk's mix has read it)
+      // LDS DMA of M3 rows.  Vector memory loads complete in issue order, so
+      // a stage's wait for its chunk's register loads covers every DMA
+      // issued before them: a chunk's M3 key and value rows are always
+      // issued before its value pieces and scales (LP1), and the score and
+      // the mix read the rows only after the stage.
       R_t R, RN;
       PageMeta cur = chunk_meta(0);
-      load_chunk(cur, R, KB0{});
       if constexpr (VM3)
         if (!is_m0(cur.vfmt)) load_value_rows(cur);
+      load_chunk(cur, R, KB0{});  // (M3 key rows first, then the register loads)
       prep_queries();
       for (int j = 0; j < total; ++j) {
         const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
@@ -1238,16 +1247,29 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
         // 162.6 us per launch for the values and scales, -> 161.6 us with
         // the codes); with two waves per SIMD the other wave covers the
         // wait, and the early values measured slower (C4: 40.7 -> 41.4 us).
+        // (a next chunk with M3 key or value rows, rare and wave-uniform,
+        // takes its register loads after those rows' DMA, at the end of the
+        // step; LP0 issues the key rows before the register loads)
+        const bool nm_vrows = VM3 && j + 1 < total && !is_m0(nm.vfmt);
+        const bool nm_rows = key_is_m3(nm) || nm_vrows;
         if constexpr (kSplitReload) {
-          load_part(nm, R, KB0{}, LP1{});
+          if (!nm_rows) load_part(nm, R, KB0{}, LP1{});
           if constexpr (KMODE != KEYS_M3) load_part(nm, RN, KB0{}, LP3{});  // (an M3 key page loads none)
         }
         score_chunk(cur, R, lds_all, KB0{}, Ls);
-        load_part(nm, R, KB0{}, std::integral_constant<int, kSplitReload ? 4 : 0>{});
+        if constexpr (kSplitReload)
+          load_part(nm, R, KB0{}, LP4{});
+        else if (!nm_vrows)
+          load_part(nm, R, KB0{}, LP0{});
         softmax_chunk(cur, Ls, pa);
         mix_chunk(cur, lds_all, pa);
         if constexpr (VM3)
-          if (j + 1 < total && !is_m0(nm.vfmt)) load_value_rows(nm);
+          if (nm_vrows) load_value_rows(nm);
+        if constexpr (kSplitReload) {
+          if (nm_rows) load_part(nm, R, KB0{}, LP1{});
+        } else if (nm_vrows) {
+          load_part(nm, R, KB0{}, LP0{});
+        }
         if constexpr (kSplitReload && KMODE != KEYS_M3)
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh)

@@ -198,7 +198,8 @@ def page_costs(k_pool: DevicePagePool, v_pool: DevicePagePool, k_table, v_table,
 
 
 def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *, device="cuda",
-              target_items: int | None = None, chunks_per_page: int = 1, page_cost=None) -> DecodePlan:
+              target_items: int | None = None, chunks_per_page: int = 1, page_cost=None,
+              last_page_tokens=None) -> DecodePlan:
     """Work and merge items for a batch with these page counts.  With
     ``pages_per_split`` the near-equal splits of ``dc_plan_decode`` (whole
     pages).  Without it ``dc_plan_decode_fill``: ``target_items`` (default:
@@ -208,6 +209,9 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     costing ``page_cost[b, h, page]`` (float ``[n_seqs, n_kv_heads, >= max
     pages]``; default: the same for every chunk).  No item has fewer than
     ``MIN_CHUNKS_PER_SPLIT`` chunks unless its stream does.
+    ``last_page_tokens`` (one per sequence, fill plans only): the tokens in
+    each sequence's last page, so the chunks past them are not counted and
+    no item falls among them; without it every page counts as full.
     ``DecodePlan.pages_per_split`` is the largest item's page count."""
     torch = _torch()
     sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
@@ -226,8 +230,13 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
         cost = np.ascontiguousarray(np.asarray(page_cost, dtype=np.float32))
         if cost.ndim != 3 or cost.shape[:2] != (sp.size, int(n_kv_heads)) or cost.shape[2] < int(sp.max()):
             raise ValueError("page_cost must have shape [n_seqs, n_kv_heads, >= max pages]")
+    last = None
+    if fill and last_page_tokens is not None:
+        last = np.ascontiguousarray(np.asarray(last_page_tokens, dtype=np.int32))
+        if last.shape != sp.shape:
+            raise ValueError("last_page_tokens must have one entry per sequence")
     key = (sp.tobytes(), int(n_kv_heads), pps, target, cpp, None if cost is None else (cost.shape, cost.tobytes()),
-           str(device))
+           None if last is None else last.tobytes(), str(device))
     hit = _plan_cache.get(key)
     if hit is not None:
         return hit
@@ -236,7 +245,8 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
 
     def plan(items_p, max_items, merges_p, max_merges):
         if fill:
-            return L.dc_plan_decode_fill(sp.ctypes.data, sp.size, n_kv_heads, cpp,
+            return L.dc_plan_decode_fill(sp.ctypes.data, None if last is None else last.ctypes.data, sp.size,
+                                         n_kv_heads, cpp,
                                          None if cost is None else cost.ctypes.data,
                                          0 if cost is None else cost.shape[2], target, MIN_CHUNKS_PER_SPLIT,
                                          items_p, max_items, C.byref(ni), merges_p, max_merges, C.byref(nm),
@@ -401,8 +411,11 @@ def decode_paged(
                 raise ValueError("key and value pages must hold the same token counts")
     cpp = chunks_per_page(pool.geometry.page_capacity)
     if plan is None:
+        last = None
+        if validate:  # the host tables are at hand: cut only chunks that hold tokens
+            last = np.asarray([pool.tokens_of(kt[b, 0, sp[b] - 1]) for b in range(B)], dtype=np.int32)
         plan = make_plan(sp, H, pages_per_split, device=queries.device, chunks_per_page=cpp,
-                         target_items=launch_target_items(pool, vpool, Q))
+                         target_items=launch_target_items(pool, vpool, Q), last_page_tokens=last)
     plan.check(sp, H, stride, cpp)
     if not queries.is_contiguous():
         queries = queries.contiguous()

@@ -290,12 +290,13 @@ class DevicePagedKVCache:
             raise ValueError("every KV head must serve the same number of query heads")
         order = np.argsort(qmap, kind="stable")  # query heads grouped by KV head
         contiguous = np.array_equal(order, np.arange(Hq))
-        k_table, v_table, seq_pages = self._layer_tables(lid)
+        k_table, v_table, seq_pages, last_tokens = self._layer_tables(lid)
         qg = q if contiguous else q[:, torch.from_numpy(order).to(self.device)]
         queries = qg.reshape(B, H, Hq // H, hd)
         plan = make_plan(seq_pages, H, device=self.device,
                          chunks_per_page=chunks_per_page(self.k_pool.geometry.page_capacity),
-                         target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H))
+                         target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H),
+                         last_page_tokens=last_tokens)
         need = workspace_bytes(plan, Hq // H, hd)
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.device)
@@ -310,8 +311,9 @@ class DevicePagedKVCache:
 
     # ---- bookkeeping -------------------------------------------------------
     def _layer_tables(self, lid: int):
-        """Device page tables of a layer: each stream's pages, then its tail
-        page when the tail holds tokens."""
+        """Device page tables of a layer (each stream's pages, then its tail
+        page when the tail holds tokens), the page counts and the tokens in
+        each sequence's last page."""
         torch = _torch()
         if self._tables[lid] is None:
             B, H = self.batch_size, self.num_key_value_heads
@@ -326,7 +328,9 @@ class DevicePagedKVCache:
                         ids = self._pages[kind][lid][b][h] + ([int(self._tail_page[kind][lid, b, h])] if has_tail[b] else [])
                         t[b, h, : len(ids)] = ids
                 tabs[kind] = torch.from_numpy(t).to(self.device)
-            self._tables[lid] = (tabs["K"], tabs["V"], counts)
+                if kind == "K":
+                    last = self.k_pool.tokens_of(t[np.arange(B), 0, np.maximum(counts - 1, 0)]).astype(np.int32)
+            self._tables[lid] = (tabs["K"], tabs["V"], counts, last)
         return self._tables[lid]
 
     def clear_layer(self, layer_id: int) -> None:
@@ -371,7 +375,7 @@ class DevicePagedKVCache:
         for lid in range(self.num_hidden_layers):
             if self._seq_len[lid, 0] == 0:
                 continue
-            k_table, v_table, counts = self._layer_tables(lid)
+            k_table, v_table, counts, _ = self._layer_tables(lid)
             kt, vt = k_table.cpu().numpy(), v_table.cpu().numpy()
             for b in range(self.batch_size):
                 total += self.k_pool.read_bytes(kt[b, :, : counts[b]]) + self.v_pool.read_bytes(vt[b, :, : counts[b]])

@@ -400,13 +400,15 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
     # per layer: a launch's budget of items cut at 32-token chunks, each
     # stream cut by its pages' costs (an exact recent window reads more
     # bytes per token)
+    # (the last pages' token counts: C5's tail holds the one appended token)
     cpp = chunks_per_page(P)
     for l, lt in enumerate(tables):
         cost = None
         if pages_per_split is None:
             cost = page_costs(k_pool, v_pool, kids_tables[l], vids_tables[l], lt.seq_pages)
+        last = k_pool.tokens_of(kids_tables[l][np.arange(B), 0, np.asarray(lt.seq_pages) - 1]).astype(np.int32)
         wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp, page_cost=cost,
-                                  target_items=launch_target_items(k_pool, v_pool, Q)))
+                                  target_items=launch_target_items(k_pool, v_pool, Q), last_page_tokens=last))
     wl.plan = wl.plans[0]
     need = max(workspace_bytes(p, Q, hd) for p in wl.plans)
     wl.workspace = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)

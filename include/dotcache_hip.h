@@ -188,8 +188,9 @@ int dc_set_encode_path(int32_t path);
 
 /* logits[q, token_offsets[i] + t] = score of query q against token t of
  * page page_ids[i], for n_queries fp32 queries [n_queries, head_dim].
- * token_offsets (device, [n_pages + 1]) is the prefix sum of page token
- * counts.  Replaces reference dotcache/attention_reference.py:34-128
+ * token_offsets (device, [n_pages]) gives where each page's logits start:
+ * the prefix sum of page token counts, or the starts of a subset of a
+ * longer row (the pages whose logits are not cached).  Replaces reference dotcache/attention_reference.py:34-128
  * (score_page_ref) behind dotcache/backends/torch_cuda.py:53-68
  * (score_page_cuda / score_pages_cuda). */
 int dc_score_pages(dc_pool pool, const int32_t* page_ids, const int32_t* token_offsets, int32_t n_pages,
@@ -274,9 +275,12 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
 /* Host-only planner that fills a launch with items of near-equal cost.
  * Each (sequence, kv_head) stream is a run of seq_pages[b] x chunks_per_page
  * chunks (32 tokens each; chunks_per_page = ceil(page_capacity / 32) lets
- * items split pages, 1 keeps them whole).  A chunk costs page_cost[(b *
- * n_kv_heads + h) * cost_stride + page] / chunks_per_page, or 1 when
- * page_cost is NULL (costs must be finite and >= 0).  Starting from one item
+ * items split pages, 1 keeps them whole), less the chunks of its last page
+ * past last_page_tokens[b] tokens (host int32 [n_seqs], each in [1, 32 x
+ * chunks_per_page]; NULL: every page counts as full), so no item is cut
+ * among chunks that hold no token.  A chunk costs page_cost[(b *
+ * n_kv_heads + h) * cost_stride + page] / (the page's counted chunks), or 1
+ * when page_cost is NULL (costs must be finite and >= 0).  Starting from one item
  * per stream, the planner adds one split at a time to the stream with the
  * largest mean item cost (ties to the longer stream, then the lower index)
  * while fewer than target_items items exist and that stream's items keep at
@@ -289,8 +293,9 @@ int dc_plan_decode(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads,
  * The chunking of the reference's grouped decode
  * (dotcache/backends/torch_mps.py:4110-4273) has no launch to fill; this
  * planner has no reference counterpart beyond it. */
-int dc_plan_decode_fill(const int32_t* seq_pages, int32_t n_seqs, int32_t n_kv_heads, int32_t chunks_per_page,
-                        const float* page_cost, int64_t cost_stride, int32_t target_items,
+int dc_plan_decode_fill(const int32_t* seq_pages, const int32_t* last_page_tokens, int32_t n_seqs,
+                        int32_t n_kv_heads, int32_t chunks_per_page, const float* page_cost, int64_t cost_stride,
+                        int32_t target_items,
                         int32_t min_chunks_per_split, dc_work_item* items, int32_t max_items, int32_t* n_items,
                         dc_merge_item* merges, int32_t max_merges, int32_t* n_merges, int32_t* n_partials,
                         int32_t* largest_item);

@@ -77,7 +77,7 @@ def test_planner_covers_every_page_once():
     assert sorted(ms) == [(0, 0, 0, 2), (0, 1, 2, 2), (2, 0, 4, 3), (2, 1, 7, 3)]
 
 
-def _plan_fill(seq_pages, heads, target, cpp=1, cost=None, min_chunks=None):
+def _plan_fill(seq_pages, heads, target, cpp=1, cost=None, min_chunks=None, last_tokens=None):
     """dc_plan_decode_fill; items as (seq, head, first chunk, end chunk,
     partial) with chunk positions counted along the stream."""
     sp = np.asarray(seq_pages, dtype=np.int32)
@@ -88,7 +88,8 @@ def _plan_fill(seq_pages, heads, target, cpp=1, cost=None, min_chunks=None):
         cost = np.ascontiguousarray(cost, dtype=np.float32)
         cp, stride = cost.ctypes.data, cost.shape[2]
     ni, nm, npart, big = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
-    args = (sp.ctypes.data, sp.size, heads, cpp, cp, stride, target, min_chunks)
+    lt = None if last_tokens is None else np.ascontiguousarray(last_tokens, dtype=np.int32)
+    args = (sp.ctypes.data, None if lt is None else lt.ctypes.data, sp.size, heads, cpp, cp, stride, target, min_chunks)
     st = L.dc_plan_decode_fill(*args, None, 0, C.byref(ni), None, 0, C.byref(nm), C.byref(npart), C.byref(big))
     if st != _lib.DC_ESPACE:
         _lib.check(st, "plan fill")
@@ -107,14 +108,16 @@ def _plan_fill(seq_pages, heads, target, cpp=1, cost=None, min_chunks=None):
     return its, ms, npart.value, big.value
 
 
-def _check_plan_shape(its, ms, npart, seq_pages, heads, cpp=1, equal=True):
+def _check_plan_shape(its, ms, npart, seq_pages, heads, cpp=1, equal=True, last_chunks=None):
     """Every (sequence, head) covers its chunks once, in order, by non-empty
     (without costs: near-equal) items; split streams own consecutive partial
-    slots named by their merge."""
+    slots named by their merge.  ``last_chunks[b]``: the chunks of sequence
+    b's last page that hold tokens (default: all)."""
     for b, n in enumerate(seq_pages):
+        live = n * cpp if last_chunks is None else (n - 1) * cpp + last_chunks[b]
         for h in range(heads):
             mine = [(u0, u1, part) for (s, hh, u0, u1, part) in its if s == b and hh == h]
-            assert [u for (u0, u1, _) in mine for u in range(u0, u1)] == list(range(n * cpp))
+            assert [u for (u0, u1, _) in mine for u in range(u0, u1)] == list(range(live))
             sizes = [u1 - u0 for (u0, u1, _) in mine]
             assert min(sizes) >= 1
             if equal:
@@ -204,6 +207,28 @@ def test_fill_planner_ragged_and_limits():
         _plan_fill([3], 1, 0)
     with pytest.raises(ValueError):  # no chunks per page
         _plan_fill([3], 1, 8, cpp=0)
+
+
+def test_fill_planner_cuts_only_chunks_that_hold_tokens():
+    """A partial last page counts only the chunks that hold tokens: 128-token
+    pages (4 chunks), last pages of 10, 33 and 128 tokens.  Without the
+    counts, four items over two pages put the last item on the 10-token
+    page's empty chunks 2 and 3."""
+    its, ms, npart, _ = _plan_fill([2], 1, 4, cpp=4, min_chunks=1)
+    assert (0, 0, 6, 8, 3) in its  # the empty tail, as an item of its own
+    its, ms, npart, big = _plan_fill([2], 1, 4, cpp=4, min_chunks=1, last_tokens=[10])
+    assert [(u0, u1) for (_, _, u0, u1, _) in its] == [(0, 1), (1, 2), (2, 3), (3, 5)] and big == 2
+    _check_plan_shape(its, ms, npart, [2], 1, cpp=4, last_chunks=[1])
+    # several sequences and heads, with and without page costs
+    sp, last = [2, 3, 5], [10, 33, 128]
+    lc = [(t + 31) // 32 for t in last]
+    for cost in (None, np.random.default_rng(0).uniform(0.5, 2.0, size=(3, 2, 5)).astype(np.float32)):
+        its, ms, npart, _ = _plan_fill(sp, 2, 24, cpp=4, cost=cost, min_chunks=1, last_tokens=last)
+        _check_plan_shape(its, ms, npart, sp, 2, cpp=4, equal=cost is None, last_chunks=lc)
+    with pytest.raises(ValueError):  # more tokens than a page holds
+        _plan_fill([2], 1, 4, cpp=4, last_tokens=[129])
+    with pytest.raises(ValueError):
+        _plan_fill([2], 1, 4, cpp=4, last_tokens=[0])
 
 
 def test_make_plan_chunk_fields_and_checks():

@@ -221,6 +221,11 @@ FAST_CASES = [
     (dict(bits=8), dict(bits=8, scheme="symmetric"), 128, 64, 6, 64),
     (dict(bits=8), dict(bits=4, scheme="symmetric"), 64, 32, 3, 64),
     (dict(bits=8, scheme="symmetric"), dict(bits=4), 256, 32, 4, 128),
+    # capacity 256 at head_dim 256: 8-bit key codes (or value codes) fill
+    # 64 KiB, so the scales sit at byte 65536 of the blob
+    (dict(bits=8), dict(bits=4), 256, 32, 4, 256),
+    (dict(bits=4), dict(bits=8, scheme="symmetric"), 256, 64, 4, 256),
+    (dict(bits=8), dict(bits=8), 256, 32, 3, 256),
 ]
 
 

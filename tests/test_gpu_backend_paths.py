@@ -122,3 +122,44 @@ def test_execution_trace_counts_page_bytes():
     tr2 = ExecutionTrace()
     rt.score_page(q[0], kpp[2], backend="hip_mi355x", trace=tr2)  # the partial page: 22 tokens
     assert tr2.device_bytes_read == 22 * 80 and tr2.payload_bytes_read == kpp[2].payload_nbytes
+
+
+def test_cached_page_logits_are_used_and_their_pages_not_read():
+    """decode_step_with_page_logits with a mix of cached and None entries
+    (reference attention_runtime.py:298-303): the cached logits differ from a
+    rescore of their pages, so the output shows they were used, and the trace
+    counts only the key pages actually scored, plus every value page."""
+    from dotcache_amd import attention_runtime as rt
+    from dotcache_amd.tracing import ExecutionTrace
+
+    rng = np.random.default_rng(1600)
+    hd = 128
+    n = 64 * 4 + 30
+    kp = _pages(hard_values(rng, n, hd), 64, hd, "K", bits=4)
+    vp = _pages(hard_values(rng, n, hd), 64, hd, "V", bits=4, scheme="symmetric")
+    kpp, vpp = [to_product_page(p) for p in kp], [to_product_page(p) for p in vp]
+    q = (rng.normal(size=hd) / np.sqrt(hd)).astype(np.float32)
+    # pages 1 and 4 (the partial one) cached, perturbed away from their true logits
+    cached = [None] * len(kp)
+    for i in (1, 4):
+        cached[i] = (O.score_page_ref(q, kp[i]) + rng.normal(scale=2.0, size=kp[i].header.token_count)).astype(np.float32)
+    tr = ExecutionTrace()
+    logits, weights, out = rt.decode_step_with_page_logits(q, kpp, vpp, page_logits=cached, backend="hip_mi355x",
+                                                           trace=tr)
+    wl, ww, wo = O.decode_step(q, kp, vp, page_logits=cached)
+    np.testing.assert_allclose(logits, wl, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(weights, ww, atol=1e-6, rtol=1e-4)
+    assert np.max(np.abs(out - wo)) < 1e-3
+    # a rescore would give a different output
+    _, _, fresh = O.decode_step(q, kp, vp)
+    assert np.max(np.abs(fresh - wo)) > 1e-2
+    scored = [p for i, p in enumerate(kpp) if cached[i] is None]
+    assert tr.payload_bytes_read == sum(p.payload_nbytes for p in scored + vpp)
+    assert tr.device_bytes_read == sum(O.page_device_nbytes(p) for i, p in enumerate(kp) if cached[i] is None) + \
+        sum(O.page_device_nbytes(p) for p in vp)
+    # every page cached: no key page is read, the output still follows the cache
+    all_cached = [O.score_page_ref(q, p) + 0.5 * rng.normal(size=p.header.token_count).astype(np.float32) for p in kp]
+    tr2 = ExecutionTrace()
+    _, _, out2 = rt.decode_step_with_page_logits(q, kpp, vpp, page_logits=all_cached, backend="hip_mi355x", trace=tr2)
+    assert np.max(np.abs(out2 - O.decode_step(q, kp, vp, page_logits=all_cached)[2])) < 1e-3
+    assert tr2.payload_bytes_read == sum(p.payload_nbytes for p in vpp)

@@ -2,7 +2,8 @@
 pools, one fused ``dc_decode_paged`` launch per layer (plus the per-step
 append for config 5), checked against the oracle run on the same pages
 downloaded from the device.  Reduced sizes cover every configuration; the
-full config 3 shape is checked on sampled (sequence, KV head) streams."""
+full shapes of configs 2 to 5 are checked on sampled (sequence, KV head)
+streams."""
 import numpy as np
 import pytest
 
@@ -103,6 +104,29 @@ def test_full_size_c3_sampled_streams():
     wl.step()
     torch.cuda.synchronize()
     _check(wl, 0, [(0, 0), (0, 3), (7, 1), (7, 2)])
+
+
+def test_full_size_c2_streams():
+    """Config 2 at its bench shape (batch 1, context 4096, page 64, GQA 4,
+    head_dim 64, affine 4-bit keys and values) with the bench's plan (a
+    launch's item budget of 2-chunk items) and its page records: every KV
+    head of two layers against the oracle."""
+    import torch
+
+    from dotcache_amd.workloads import build_workload
+
+    wl = build_workload("c2", seed=0, layers=2)
+    assert wl.spec.batch == 1 and int(wl.lengths[0]) == 4096 and wl.spec.head_dim == 64
+    plan = wl.plans[0]
+    assert wl.records, "the workload gathers page records for its plans"
+    # 8 streams of 64 pages (128 chunks) in 512 items of 2 chunks
+    assert plan.n_items == 512 and plan.largest_chunks == 2, (plan.n_items, plan.largest_chunks)
+    print(f"c2 full: {plan.n_items} items per layer, largest {plan.largest_chunks} chunks", flush=True)
+    wl.step()
+    torch.cuda.synchronize()
+    H = wl.spec.n_kv_heads
+    for layer in range(2):
+        _check(wl, layer, [(0, h) for h in range(H)])
 
 
 @pytest.mark.parametrize("name,context", [("c2", 700), ("c5", 1000)])
