@@ -210,23 +210,62 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(wl, budget_s: float) -> dict:
+# token positions of one (sequence, KV head) stream that a CPU sample slice
+# covers at most (config 3's whole stream), so that one slice of a 131K-token
+# config 5 stream stays a few seconds of oracle time
+CPU_SLICE_TOKENS = 16384
+
+
+def _oracle_worker_init():
+    """Imports of an all-cores baseline worker, done before the clock starts."""
+    import threadpoolctl  # noqa: F401
+
+    from oracle import dotcache_oracle  # noqa: F401
+
+
+def _oracle_stream_worker(job):
+    """One worker of the all-cores baseline: decode every stream of ``job``
+    (oracle pages and queries, every GQA head) with BLAS on one thread,
+    starting at wall-clock time ``start_at``; returns (tokens, end time)."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import dotcache_oracle as O
+
+    streams, start_at = job
+    while time.time() < start_at:  # every worker starts together
+        time.sleep(0.0005)
+    tokens = 0
+    with threadpool_limits(limits=1):
+        for qs, kp, vp in streams:
+            for q in qs:
+                O.decode_step(q, kp, vp)
+            tokens += sum(p.header.token_count for p in kp)
+    return tokens, time.time()
+
+
+def cpu_baseline(wl, budget_s: float, all_cores: bool = True) -> dict:
     """Time the CPU oracle (numpy restatement of the reference cpu_ref path:
     per page score, one global softmax, per page mix, one query head at a
     time) on a bounded sample of the same workload: layer 0's (sequence, KV
-    head) streams in order, every GQA query head of each.  Two slices of the
-    same streams check that the cost per token position is linear in the
-    context: first each stream cut to half its pages (a third of the
-    budget), then the whole streams (the rest).  One (sequence, layer,
-    token) position covers all KV heads, so a rate is tokens done / KV heads
-    / seconds; ``value`` is the whole-stream slice's."""
+    head) streams in order, every GQA query head of each, each stream cut to
+    at most CPU_SLICE_TOKENS tokens.  Two slices of the same streams check
+    that the cost per token position is linear in the context: first each
+    stream cut to half its slice (a third of the budget), then the whole
+    slices (the rest).  One (sequence, layer, token) position covers all KV
+    heads, so a rate is tokens done / KV heads / seconds; ``value`` is the
+    whole-slice rate on one core.  ``all_cores``: the same slices spread over
+    one worker process per visible CPU (at most 16, the GPU box's share),
+    each on one BLAS thread, timed by the wall clock from a common start."""
+    import multiprocessing as mp
+
     from threadpoolctl import threadpool_limits
 
     from oracle import dotcache_oracle as O
 
     spec = wl.spec
     lt = wl.layers[0]
-    H, Q = spec.n_kv_heads, spec.gqa
+    H, Q, P = spec.n_kv_heads, spec.gqa, spec.page_size
+    cap_pages = max(1, -(-CPU_SLICE_TOKENS // P))
     q_all = wl.queries[0].float().cpu().numpy() * wl.query_scale  # [B, H, Q, hd]
 
     def to_oracle(pool, pid, kind):
@@ -235,25 +274,30 @@ def cpu_baseline(wl, budget_s: float) -> dict:
         return O.OraclePage(header=oh, payload=page.payload, scales=page.scales, bias=page.bias,
                             escape_payload=page.escape_payload, escape_scales=page.escape_scales)
 
+    def stream(b, h, fraction):
+        n = min(int(lt.seq_pages[b]), cap_pages)
+        keep = max(1, int(round(n * fraction)))
+        kt = lt.k_table[b].cpu().numpy()
+        vt = lt.v_table[b].cpu().numpy()
+        kp = [to_oracle(wl.k_pool, kt[h, p], "K") for p in range(keep)]
+        vp = [to_oracle(wl.v_pool, vt[h, p], "V") for p in range(keep)]
+        return [q_all[b, h, j] for j in range(Q)], kp, vp
+
+    order = [(b, h) for b in range(spec.batch) for h in range(H)]
+
     def run(fraction: float, budget: float):
         tokens = streams = 0
         dt = 0.0
-        for b in range(spec.batch):
-            n = int(lt.seq_pages[b])
-            keep = max(1, int(round(n * fraction)))
-            kt = lt.k_table[b].cpu().numpy()
-            vt = lt.v_table[b].cpu().numpy()
-            for h in range(H):
-                kp = [to_oracle(wl.k_pool, kt[h, p], "K") for p in range(keep)]
-                vp = [to_oracle(wl.v_pool, vt[h, p], "V") for p in range(keep)]
-                t0 = time.perf_counter()
-                for j in range(Q):
-                    O.decode_step(q_all[b, h, j], kp, vp)
-                dt += time.perf_counter() - t0
-                tokens += sum(p.header.token_count for p in kp)
-                streams += 1
-                if dt > budget:
-                    return tokens, streams, dt
+        for b, h in order:
+            qs, kp, vp = stream(b, h, fraction)
+            t0 = time.perf_counter()
+            for q in qs:
+                O.decode_step(q, kp, vp)
+            dt += time.perf_counter() - t0
+            tokens += sum(p.header.token_count for p in kp)
+            streams += 1
+            if dt > budget:
+                break
         return tokens, streams, dt
 
     with threadpool_limits(limits=1):
@@ -261,7 +305,7 @@ def cpu_baseline(wl, budget_s: float) -> dict:
         tokens, streams, dt = run(1.0, budget_s * 2 / 3)
     rate = tokens / H / dt
     rate_half = t_half / H / dt_half
-    return {
+    out = {
         "value": rate,
         "unit": "KV tokens/s",
         "cores": 1,
@@ -270,11 +314,35 @@ def cpu_baseline(wl, budget_s: float) -> dict:
         "host_cpus": os.cpu_count(),
         "linearity": {"half_context_tokens_per_s": rate_half, "full_context_tokens_per_s": rate,
                       "ratio_full_over_half": rate / rate_half},
-        "sample": f"layer 0: {streams} whole (sequence, KV head) streams x {Q} query heads, {tokens} tokens, "
-                  f"{dt:.1f} s of oracle time (page downloads excluded), after {s_half} streams cut to half their "
-                  f"pages ({t_half} tokens, {dt_half:.1f} s) for the linearity check; numpy oracle of reference "
-                  f"cpu_ref, one thread (BLAS pinned to 1), on {cpu_model()} ({os.cpu_count()} cpus visible)",
+        "sample": f"layer 0: {streams} (sequence, KV head) streams of at most {cap_pages * P} tokens x {Q} query "
+                  f"heads, {tokens} tokens, {dt:.1f} s of oracle time (page downloads excluded), after {s_half} "
+                  f"streams cut to half that ({t_half} tokens, {dt_half:.1f} s) for the linearity check; numpy "
+                  f"oracle of reference cpu_ref, one thread (BLAS pinned to 1), on {cpu_model()} "
+                  f"({os.cpu_count()} cpus visible)",
     }
+    if all_cores:
+        workers = max(1, min(os.cpu_count() or 1, 16))
+        per = max(1, -(-max(streams, 2) // 2))  # about half the one-core sample per worker
+        jobs = []
+        for w in range(workers):
+            picks = [order[(w * per + i) % len(order)] for i in range(per)]
+            jobs.append([stream(b, h, 1.0) for b, h in picks])
+        # fresh interpreters (spawn: started as child programs, with no GPU
+        # state), their imports done by the initializer before the clock
+        ctx = mp.get_context("spawn")
+        with ctx.Pool(workers, initializer=_oracle_worker_init) as pool:
+            pool.map(abs, range(4 * workers), chunksize=1)
+            start_at = time.time() + 2.0  # jobs are pickled and handed out meanwhile
+            res = pool.map(_oracle_stream_worker, [(j, start_at) for j in jobs], chunksize=1)
+        done = sum(r[0] for r in res)
+        wall = max(r[1] for r in res) - start_at  # common start to the last worker's end
+        out["all_cores"] = {
+            "value": done / H / wall,
+            "cores": workers,
+            "sample": f"{workers} worker processes x {per} streams each (the one-core slices), {done} tokens, "
+                      f"{wall:.1f} s wall from a common start to the last worker's end, one BLAS thread per worker",
+        }
+    return out
 
 
 def main():
@@ -426,7 +494,8 @@ def main():
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline ...")
         cpu = cpu_baseline(wl, args.cpu_seconds)
-        log(f"cpu baseline {cpu['value']:.0f} tokens/s ({cpu['sample']})")
+        log(f"cpu baseline {cpu['value']:.0f} tokens/s ({cpu['sample']})"
+            + (f"; all cores {cpu['all_cores']['value']:.0f} tokens/s ({cpu['all_cores']['sample']})" if "all_cores" in cpu else ""))
 
     fmt = lambda f: f"{f.mode} fp16" if f.mode == "M3" else f"M0 {f.scheme} int{f.bits} g{f.group_size}"
     line = {

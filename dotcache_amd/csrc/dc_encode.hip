@@ -13,7 +13,11 @@
 //     loads its channels with 16-byte loads, a group's min / max / max |x|
 //     is a butterfly over the group's lanes, and a lane's 8 codes are one
 //     word at 4 bits and two at 8 bits, stored as they are; 2- and 3-bit
-//     words (which lanes share) are OR-ed together in LDS.  Taken when the
+//     words (which lanes share) are OR-ed together in LDS.  A code comes
+//     from the reciprocal of its group's scale, and from the correctly
+//     rounded division only where that could round differently
+//     (rint_quotients8: the same bits, about 5 instead of 13 instructions
+//     per code).  Taken when the
 //     group size and head_dim are multiples of 8 and the padded head_dim / 8
 //     and group size / 8 are powers of two (every configuration here).
 //   encode_rows_kernel (the general path): one thread per (row, group),
@@ -136,6 +140,38 @@ struct EncodeJob {
 constexpr int kEncThreads = 256;
 // LDS words per wavefront for 2- / 3-bit packing
 constexpr int kPackWords = 64;
+typedef _Float16 enc_h2 __attribute__((ext_vector_type(2)));
+// row blocks (kEncThreads / 64 wavefronts x one row per lane group) per
+// workgroup of encode_rows8_kernel, their loads all in flight together
+constexpr int kEncRowBlocks = 2;
+
+// q[i] = rintf(d[i] / s) (the correctly rounded quotient, rounded half to
+// even: the reference's np.round of an fp32 division) from a reciprocal.
+// With rcp = v_rcp_f32(s), within 1 ulp (2^-23 relative) of 1 / s, the
+// product y = d rcp (one more rounding, 2^-24) lies within |y| 2^-22 of
+// fl(d / s) (whose own rounding adds the last 2^-24), so rint(y) =
+// rint(fl(d / s)) unless a half-integer lies that close to y.  The nearest
+// half-integer is |y - rint(y)| from 1/2 away; if any of the lane's 8
+// values comes within twice that distance (|y - rint(y)| + |y| 2^-21 >=
+// 1/2, one fma whose own rounding, 2^-24 relative, stays far inside the
+// margin), or exact is set, all 8 take the correctly rounded division
+// instead (a branch the lane rarely takes: for uniform data about |y|
+// 2^-20 of the codes are that close; the empty asm keeps the compiler from
+// running the divisions unconditionally).
+__device__ __forceinline__ void rint_quotients8(const float (&d)[8], float s, float rcp, bool exact, float (&q)[8]) {
+  float e = 0.f;  // the largest |y - rint(y)| + |y| 2^-21 of the 8
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float y = d[i] * rcp;
+    q[i] = rintf(y);
+    e = fmaxf(e, __builtin_fmaf(fabsf(y), 0x1p-21f, fabsf(y - q[i])));
+  }
+  if (exact || e >= 0.5f) {
+    asm volatile("");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = rintf(d[i] / s);
+  }
+}
 
 __device__ __forceinline__ float seg_min(float v, int lanes) {
   for (int o = 1; o < lanes; o <<= 1) v = fminf(v, __shfl_xor(v, o, 64));
@@ -148,20 +184,21 @@ __device__ __forceinline__ float seg_max(float v, int lanes) {
 
 // Eight consecutive values of row r from channel c0 (dtype DC_F32 / F16 /
 // BF16); vec: the row start is 16-byte aligned for this dtype.
-__device__ __forceinline__ void load8(const void* values, int32_t dtype, int64_t off, bool vec, float* x) {
-  if (dtype == DC_F32) {
+template <int32_t dtype, bool vec>
+__device__ __forceinline__ void load8(const void* values, int64_t off, float* x) {
+  if constexpr (dtype == DC_F32) {
     const float* p = reinterpret_cast<const float*>(values) + off;
-    if (vec) {
+    if constexpr (vec) {
       const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
       x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
       return;
     }
-  } else if (vec) {
+  } else if constexpr (vec) {
     const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(values) + off);
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (dtype == DC_F16) {
+      if constexpr (dtype == DC_F16) {
         x[2 * i] = __half2float(__ushort_as_half(uint16_t(w[i] & 0xffffu)));
         x[2 * i + 1] = __half2float(__ushort_as_half(uint16_t(w[i] >> 16)));
       } else {
@@ -175,80 +212,89 @@ __device__ __forceinline__ void load8(const void* values, int32_t dtype, int64_t
   for (int i = 0; i < 8; ++i) x[i] = load_value(values, dtype, off + i);
 }
 
-// blockIdx.y selects the job (K rows, V rows).  Row r of the job is handled
-// by lanes [lpr * (r % rpw), ...) of wavefront r / rpw, lpr = padded
-// head_dim / 8 lanes per row, rpw = 64 / lpr rows per wavefront.
-__global__ void __launch_bounds__(kEncThreads) encode_rows8_kernel(EncodeJob j0, EncodeJob j1, int32_t dtype,
-                                                                   int64_t n_rows, int64_t row_stride, int32_t vec,
-                                                                   int32_t lds_pack) {
-  __shared__ uint32_t pack[kEncThreads / 64][kPackWords];
-  const EncodeJob J = blockIdx.y == 0 ? j0 : j1;
+// One row's part of encode_rows8_kernel: lane (q, rw) encodes channels
+// c0 .. c0 + 7 of the row into slot t of the page d describes.
+__device__ __forceinline__ void encode_row(const EncodeJob& J, const float (&x)[8], int32_t t, const dc_page_desc& d,
+                                           bool live, uint32_t (*pack)[kPackWords], int32_t lds_pack, int lane,
+                                           int wave, int q, int rw, int32_t c0, int32_t g, int32_t li, int lpr,
+                                           int lpg) {
   const dc_page_geometry geo = J.pool.geometry;
   const int32_t hd = geo.head_dim, gs = geo.group_size, C = geo.page_capacity;
-  const int32_t G = (hd + gs - 1) / gs, Gp = G * gs;
-  const int lpr = Gp / 8, lpg = gs / 8, rpw = 64 / lpr;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int q = lane % lpr, rw = lane / lpr;  // lane within its row, row within the wavefront
-  const int64_t r = (int64_t(blockIdx.x) * (kEncThreads / 64) + wave) * rpw + rw;
-  const int32_t c0 = 8 * q, g = c0 / gs, li = (c0 - g * gs) / 8;
-
-  // the row's page and slot; rows that do not exist or name no valid
-  // destination stay idle (they still reach the block barriers)
-  bool live = rw < rpw && r < n_rows;
-  dc_page_desc d{};
-  int32_t t = 0;
-  BlobLayout L{};
-  uint8_t* blob = nullptr;
-  if (live) {
-    const int32_t pid = J.row_page[r];
-    t = J.row_slot[r];
-    live = pid >= 0 && pid < J.pool.n_descs && t >= 0 && t < C;
-    if (live) {
-      d = J.pool.descs[pid];
-      L = blob_layout(d.format, d.bits, geo);
-      live = (int64_t(d.block) << 8) + L.total <= J.pool.arena_bytes;
-      blob = reinterpret_cast<uint8_t*>(J.pool.arena) + (uint64_t(d.block) << 8);
-    }
-  }
-  float x[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = 0.f;
-  if (live && c0 < hd) load8(J.values, dtype, r * row_stride + c0, vec != 0, x);  // channels past hd: zero padding
+  const int32_t G = (hd + gs - 1) / gs;
+  const BlobLayout L = blob_layout(d.format, d.bits, geo);
+  live = live && (int64_t(d.block) << 8) + L.total <= J.pool.arena_bytes;
+  uint8_t* blob = reinterpret_cast<uint8_t*>(J.pool.arena) + (uint64_t(d.block) << 8);
 
   const bool m0 = live && is_m0(d.format);
   uint32_t w0 = 0, w1 = 0;  // this lane's code bits (8 codes, little-endian)
-  int bits = d.bits;
+  const int bits = d.bits;
   if (m0) {
-    float lo = x[0], hi = x[0], am = fabsf(x[0]);
-#pragma unroll
-    for (int i = 1; i < 8; ++i) {
-      lo = fminf(lo, x[i]);
-      hi = fmaxf(hi, x[i]);
-      am = fmaxf(am, fabsf(x[i]));
-    }
-    lo = seg_min(lo, lpg);
-    hi = seg_max(hi, lpg);
-    am = seg_max(am, lpg);
-    const uint32_t top = (1u << bits) - 1u;
     const bool affine = d.format == DC_FMT_M0_AFFINE;
+    // the group's min and max (affine) or max |x| (symmetric), over its lanes
+    float lo = 0.f, hi = 0.f, am = 0.f;
+    if (affine) {
+      lo = x[0];
+      hi = x[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) {
+        lo = fminf(lo, x[i]);
+        hi = fmaxf(hi, x[i]);
+      }
+      lo = seg_min(lo, lpg);
+      hi = seg_max(hi, lpg);
+    } else {
+      am = fabsf(x[0]);
+#pragma unroll
+      for (int i = 1; i < 8; ++i) am = fmaxf(am, fabsf(x[i]));
+      am = seg_max(am, lpg);
+    }
+    const uint32_t top = (1u << bits) - 1u;
     const int32_t qmax = (1 << (bits - 1)) - 1;
     const float scale = affine ? fmaxf((hi - lo) / float(top), 1e-8f) : fmaxf(am / float(qmax > 1 ? qmax : 1), 1e-8f);
-    uint64_t acc = 0;
+    float dv[8], qq[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t code;
-      if (affine) {
-        const float qv = rintf((x[i] - lo) / scale);
-        code = uint32_t(fminf(fmaxf(qv, 0.f), float(top)));
-      } else {
-        const float qv = fminf(fmaxf(rintf(x[i] / scale), -float(qmax)), float(qmax));
-        const int32_t sc = int32_t(qv) + qmax;
-        code = uint32_t(sc < 0 ? 0 : (sc > int32_t(top) ? int32_t(top) : sc));
+    for (int i = 0; i < 8; ++i) dv[i] = affine ? x[i] - lo : x[i];
+    // (scale >= 1e-8: normal, and so is its reciprocal)
+    rint_quotients8(dv, scale, __builtin_amdgcn_rcpf(scale), false, qq);
+    if (bits >= 4) {
+      // 4- and 8-bit codes as bytes (v_cvt_pk_u8_f32 of exact integers),
+      // then 4-bit pairs into nibbles.  The reference's clip never binds
+      // here: d <= fl(hi - lo) and s >= fl(hi - lo) / top (1 - 2^-24) keep
+      // y below top (1 + 2^-21) < top + 1/2, and |x| <= max|x| keeps |y|
+      // below qmax + 1/2 (a floored scale only makes y smaller), so
+      // rint(y) is in [0, top] (affine) or [-qmax, qmax] (symmetric).
+      const float zp = affine ? 0.f : float(qmax);
+      uint32_t lo4 = 0, hi4 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lo4 = __builtin_amdgcn_cvt_pk_u8_f32(qq[i] + zp, uint32_t(i), lo4);
+        hi4 = __builtin_amdgcn_cvt_pk_u8_f32(qq[i + 4] + zp, uint32_t(i), hi4);
       }
-      acc |= uint64_t(code) << (i * bits);
+      if (bits == 8) {
+        w0 = lo4;
+        w1 = hi4;
+      } else {
+        // byte 2j of (b | b >> 4) is code 2j | code 2j+1 << 4
+        w0 = __builtin_amdgcn_perm(hi4 | (hi4 >> 4), lo4 | (lo4 >> 4), 0x06040200u);
+      }
+    } else {
+      uint64_t acc = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t code;
+        const float qv = qq[i];
+        if (affine) {
+          code = uint32_t(fminf(fmaxf(qv, 0.f), float(top)));
+        } else {
+          const float qc = fminf(fmaxf(qv, -float(qmax)), float(qmax));
+          const int32_t sc = int32_t(qc) + qmax;
+          code = uint32_t(sc < 0 ? 0 : (sc > int32_t(top) ? int32_t(top) : sc));
+        }
+        acc |= uint64_t(code) << (i * bits);
+      }
+      w0 = uint32_t(acc);
+      w1 = uint32_t(acc >> 32);
     }
-    w0 = uint32_t(acc);
-    w1 = uint32_t(acc >> 32);
     uint32_t* payload = reinterpret_cast<uint32_t*>(blob);
     const int64_t wb = geo.layout == 0 ? (int64_t(g) * C + t) * L.words : (int64_t(t) * G + g) * L.words;
     if (bits == 4) {
@@ -265,9 +311,8 @@ __global__ void __launch_bounds__(kEncThreads) encode_rows8_kernel(EncodeJob j0,
     if (d.format == DC_FMT_M3_F16) {
       uint32_t h[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        h[i] = uint32_t(__half_as_ushort(__float2half_rn(x[2 * i]))) |
-               (uint32_t(__half_as_ushort(__float2half_rn(x[2 * i + 1]))) << 16);
+      for (int i = 0; i < 4; ++i)  // (one v_cvt_pk_f16_f32 per pair, round to nearest even)
+        h[i] = __builtin_bit_cast(uint32_t, enc_h2{(_Float16)x[2 * i], (_Float16)x[2 * i + 1]});
       *reinterpret_cast<uint4*>(reinterpret_cast<__half*>(blob) + e) = uint4{h[0], h[1], h[2], h[3]};
     } else if (d.format == DC_FMT_M3_F32) {
       float* o = reinterpret_cast<float*>(blob) + e;
@@ -284,9 +329,13 @@ __global__ void __launch_bounds__(kEncThreads) encode_rows8_kernel(EncodeJob j0,
     const float sv = __half2float(s16);
     if (c0 < hd) {
       uint32_t b[2] = {0u, 0u};
+      // (sv may be 0: fp16 flushes 1e-8 to zero, and x / 0 must give the
+      // reference's +-inf / nan, so that row takes the division)
+      float qq[8];
+      rint_quotients8(x, sv, __builtin_amdgcn_rcpf(sv), !(sv > 0.f), qq);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float qv = fminf(fmaxf(rintf(x[i] / sv), -127.f), 127.f);
+        const float qv = fminf(fmaxf(qq[i], -127.f), 127.f);
         b[i >> 2] |= (uint32_t(int32_t(qv)) & 0xffu) << (8 * (i & 3));
       }
       *reinterpret_cast<uint2*>(blob + int64_t(t) * hd + c0) = uint2{b[0], b[1]};
@@ -314,6 +363,61 @@ __global__ void __launch_bounds__(kEncThreads) encode_rows8_kernel(EncodeJob j0,
     const int64_t wb = geo.layout == 0 ? (int64_t(g) * C + t) * L.words : (int64_t(t) * G + g) * L.words;
     for (int w = 0; w < L.words; ++w) payload[wb + w] = pack[wave][rw * wpr + g * L.words + w];
   }
+}
+
+// blockIdx.y selects the job (K rows, V rows).  Row r of the job is handled
+// by lanes [lpr * (r % rpw), ...) of wavefront r / rpw, lpr = padded
+// head_dim / 8 lanes per row, rpw = 64 / lpr rows per wavefront.
+// (Measured on the bulk encode of a C3 layer, 708.8 MB per launch: walking
+// several row blocks per wavefront with the next block's loads in flight
+// took 202 us, and giving each XCD one contiguous slice of the rows 220 us,
+// against 170 us for one row block per wavefront in launch order.)
+template <int32_t dtype, bool vec>
+__global__ void __launch_bounds__(kEncThreads) encode_rows8_kernel(EncodeJob j0, EncodeJob j1, int64_t n_rows,
+                                                                   int64_t row_stride, int32_t lds_pack) {
+  __shared__ uint32_t pack[kEncThreads / 64][kPackWords];
+  const EncodeJob J = blockIdx.y == 0 ? j0 : j1;
+  const dc_page_geometry geo = J.pool.geometry;
+  const int32_t hd = geo.head_dim, gs = geo.group_size, C = geo.page_capacity;
+  const int32_t G = (hd + gs - 1) / gs, Gp = G * gs;
+  const int lpr = Gp / 8, lpg = gs / 8, rpw = 64 / lpr;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane % lpr, rw = lane / lpr;  // lane within its row, row within the wavefront
+  const int32_t c0 = 8 * q, g = c0 / gs, li = (c0 - g * gs) / 8;
+
+  // The workgroup's kEncRowBlocks row blocks: every row's page, slot and
+  // values in one round of loads, from a clamped row and channel so that no
+  // load waits on a branch (the values array has n_rows >= 1 rows, hd is a
+  // multiple of 8), then the pages' descriptors (a clamped id:
+  // J.pool.n_descs >= 1): two dependent rounds, with kEncRowBlocks rows'
+  // loads in flight per lane.  Rows that do not exist or name no valid
+  // destination stay idle (they still reach the block barriers).
+  int32_t pid[kEncRowBlocks], ts[kEncRowBlocks];
+  float xs[kEncRowBlocks][8];
+  bool ok[kEncRowBlocks];
+#pragma unroll
+  for (int u = 0; u < kEncRowBlocks; ++u) {
+    const int64_t r = ((int64_t(blockIdx.x) * kEncRowBlocks + u) * (kEncThreads / 64) + wave) * rpw + rw;
+    const bool in_rows = rw < rpw && r < n_rows;
+    const int64_t rr = in_rows ? r : 0;
+    pid[u] = J.row_page[rr];
+    ts[u] = J.row_slot[rr];
+    float y[8];
+    load8<dtype, vec>(J.values, rr * row_stride + (c0 < hd ? c0 : 0), y);
+    const bool has = in_rows && c0 < hd;  // channels past hd: zero padding
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[u][i] = has ? y[i] : 0.f;
+    ok[u] = in_rows;
+  }
+  dc_page_desc ds[kEncRowBlocks];
+#pragma unroll
+  for (int u = 0; u < kEncRowBlocks; ++u) {
+    ok[u] = ok[u] && pid[u] >= 0 && pid[u] < J.pool.n_descs && ts[u] >= 0 && ts[u] < C;
+    ds[u] = J.pool.descs[ok[u] ? pid[u] : 0];
+  }
+#pragma unroll
+  for (int u = 0; u < kEncRowBlocks; ++u) encode_row(J, xs[u], ts[u], ds[u], ok[u], pack, lds_pack, lane, wave, q,
+                                                     rw, c0, g, li, lpr, lpg);
 }
 
 // Whether a pool's geometry fits encode_rows8_kernel: 8-channel lanes that
@@ -355,17 +459,28 @@ static int encode_launch(const EncodeJob* jobs, int n_jobs, int32_t dtype, int64
   }
   const bool all_fast = fast[0] && (n_jobs < 2 || fast[1]);
   if (fast[0] || (n_jobs > 1 && fast[1])) {
-    const int64_t blocks = (n_rows + rows_per_block - 1) / rows_per_block;
+    const int64_t blocks = (n_rows + int64_t(rows_per_block) * kEncRowBlocks - 1) / (int64_t(rows_per_block) * kEncRowBlocks);
     if (blocks > 0x7fffffff) return fail(DC_EINVAL, "too many rows");
-    if (all_fast) {
-      hipLaunchKernelGGL(encode_rows8_kernel, dim3(uint32_t(blocks), uint32_t(n_jobs)), dim3(kEncThreads), 0, stream,
-                         jobs[0], n_jobs > 1 ? jobs[1] : jobs[0], dtype, n_rows, row_stride, int32_t(vec),
-                         int32_t(narrow));
-    } else {
-      const EncodeJob& f = fast[0] ? jobs[0] : jobs[1];
-      hipLaunchKernelGGL(encode_rows8_kernel, dim3(uint32_t(blocks), 1), dim3(kEncThreads), 0, stream, f, f, dtype,
-                         n_rows, row_stride, int32_t(vec), int32_t(narrow));
-    }
+    // (one instance per input dtype and alignment: the loads carry no branch)
+    const EncodeJob& a = all_fast ? jobs[0] : (fast[0] ? jobs[0] : jobs[1]);
+    const EncodeJob& b = all_fast && n_jobs > 1 ? jobs[1] : a;
+    const dim3 grid(uint32_t(blocks), all_fast ? uint32_t(n_jobs) : 1u);
+#define DC_ENC8(DT_, VEC_)                                                                                     \
+  hipLaunchKernelGGL((encode_rows8_kernel<DT_, VEC_>), grid, dim3(kEncThreads), 0, stream, a, b, n_rows, row_stride, \
+                     int32_t(narrow))
+    if (dtype == DC_F32 && vec)
+      DC_ENC8(DC_F32, true);
+    else if (dtype == DC_F32)
+      DC_ENC8(DC_F32, false);
+    else if (dtype == DC_F16 && vec)
+      DC_ENC8(DC_F16, true);
+    else if (dtype == DC_F16)
+      DC_ENC8(DC_F16, false);
+    else if (vec)
+      DC_ENC8(DC_BF16, true);
+    else
+      DC_ENC8(DC_BF16, false);
+#undef DC_ENC8
     if (int rc = check_hip(hipGetLastError(), "encode_rows8_kernel launch")) return rc;
   }
   for (int i = 0; i < n_jobs; ++i) {
@@ -384,6 +499,7 @@ static int check_encode_args(const void* values, int32_t dtype, int64_t n_rows, 
                              const int32_t* row_page, const int32_t* row_slot, const dc_pool& pool, const char* who) {
   if (int rc = validate_geometry(pool.geometry)) return rc;
   if (!values || !row_page || !row_slot || !pool.arena || !pool.descs) return fail(DC_EINVAL, "%s: null pointer", who);
+  if (pool.n_descs <= 0) return fail(DC_EINVAL, "%s: the pool has no pages to write rows into", who);
   if (row_stride < pool.geometry.head_dim) return fail(DC_EINVAL, "%s: row_stride is smaller than head_dim", who);
   return DC_OK;
 }

@@ -215,6 +215,89 @@ def test_wavefront_encode_matches_general_kernel_and_oracle(hd, gs, dtype, strid
                 np.testing.assert_array_equal(a.escape_scales[rows].view(np.uint16), want.escape_scales.view(np.uint16))
 
 
+
+
+def tie_rows(rng, T, hd, gs, fmt):
+    """Rows whose codes sit on rounding ties and within a few ulps of them.
+    Even rows use a power-of-two scale (s = 2^e, the group's range set by
+    channels 0 and 1, so fl(range / top) = s exactly and (k + 1/2) s is an
+    exact tie); odd rows a random scale, where fl(d / s) lands on or next to
+    k + 1/2 as the fp32 arithmetic has it.  Every value is then left on the
+    tie or moved by a few ulps: 1 or 2 (inside the wavefront kernel's
+    division zone) up to 64 (outside it)."""
+    mode, scheme, bits = fmt
+    x = np.zeros((T, hd), np.float32)
+    top = 2 ** bits - 1 if mode == "M0" else 127
+    qmax = 2 ** (bits - 1) - 1 if mode == "M0" else 127
+    span = gs if mode == "M0" else hd  # int8 escapes: one scale per row
+    for t in range(T):
+        for base in range(0, hd, span):
+            n = min(span, hd - base)
+            s = np.float32(2.0 ** int(rng.integers(-6, 3))) if t % 2 == 0 else np.float32(rng.uniform(0.01, 3.0))
+            if mode == "M0" and scheme == "affine":
+                lo = np.float32(0.0) if t % 4 == 0 else np.float32(rng.uniform(-2, 2))
+                x[t, base], x[t, base + 1] = lo, np.float32(lo + np.float32(top) * s)
+                vals = lo + (rng.integers(0, top, size=n - 2).astype(np.float32) + np.float32(0.5)) * s
+            else:
+                x[t, base], x[t, base + 1] = np.float32(qmax) * s, -np.float32(qmax) * s
+                vals = (rng.integers(-qmax, qmax, size=n - 2).astype(np.float32) + np.float32(0.5)) * s
+            vals = vals.astype(np.float32)
+            ks = rng.choice([-64, -9, -3, -2, -1, 0, 0, 0, 1, 2, 3, 9, 64], size=n - 2).astype(np.float32)
+            x[t, base + 2: base + n] = (vals + ks * np.spacing(vals)).astype(np.float32)
+    return x
+
+
+TIE_FMTS = [("M0", "affine", b) for b in (2, 3, 4, 8)] + [("M0", "symmetric", b) for b in (2, 3, 4, 8)] + [
+    ("M3", "int8", 0)]
+
+
+@pytest.mark.parametrize("fmt", TIE_FMTS, ids=lambda f: f"{f[0]}-{f[1]}-{f[2]}")
+def test_encode_codes_on_and_next_to_ties(fmt):
+    """Codes whose fp32 quotient d / s is a rounding tie (k + 1/2, rounded
+    half to even) or a few ulps from one: the wavefront kernel (codes from
+    the reciprocal of the scale, the division only near ties) and the
+    general kernel (the division always) give the oracle's bytes."""
+    torch = _torch()
+    from dotcache_amd.page_pool import DevicePagePool, PoolGeometry, set_encode_path
+
+    rng = np.random.default_rng(sum(map(ord, str(fmt))))
+    hd, gs, T = 128, 32, 64
+    x = tie_rows(rng, T, hd, gs, fmt)
+    mode, sch, bits = fmt
+    want = O.encode_page(x, head_dim=hd, group_size=gs, kind="K", mode=mode,
+                         scheme="affine" if mode == "M3" else sch, bits=bits or 4,
+                         escape_dtype=sch if mode == "M3" else "float16")
+    slots = np.arange(T)
+    for path in ("auto", "general"):
+        set_encode_path(path)
+        try:
+            pool = DevicePagePool(PoolGeometry(hd, gs, 64), reserve_bytes=1 << 22)
+            (got,) = _encode_all(pool, [fmt], torch.from_numpy(x).cuda(), slots)
+        finally:
+            set_encode_path("auto")
+        if mode == "M0":
+            np.testing.assert_array_equal(got.payload, want.payload, err_msg=f"{path} codes")
+            np.testing.assert_array_equal(got.scales.view(np.uint16), want.scales.view(np.uint16))
+        else:
+            np.testing.assert_array_equal(got.escape_payload.view(np.uint8), want.escape_payload.view(np.uint8),
+                                          err_msg=f"{path} int8 codes")
+            np.testing.assert_array_equal(got.escape_scales.view(np.uint16), want.escape_scales.view(np.uint16))
+
+
+def test_tie_rows_hit_exact_ties():
+    """The tie generator's even rows put exact ties in front of the encoder:
+    with the oracle's own fp32 arithmetic, many quotients are exactly k + 1/2."""
+    rng = np.random.default_rng(5)
+    x = tie_rows(rng, 8, 128, 32, ("M0", "affine", 4))
+    ties = 0
+    for t in range(0, 8, 2):  # the power-of-two rows
+        for g in x[t].reshape(4, 32):
+            lo, s = g.min(), np.float32((g.max() - g.min()) / np.float32(15))
+            q = ((g - lo) / s).astype(np.float32)
+            ties += int(np.sum(np.abs(q - np.floor(q) - 0.5) == 0))
+    assert ties >= 40, ties  # about 3 / 13 of 16 x 30 values
+
+
 def test_encode_rows_kv_equals_two_calls():
     """dc_encode_rows_kv (keys and values in one launch, different pools,
     value group 64) writes exactly what two dc_encode_rows calls write."""
