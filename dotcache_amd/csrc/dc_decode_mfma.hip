@@ -450,6 +450,12 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
     if constexpr (KMODE == KEYS_M0) return false;
     return m.kfmt == DC_FMT_M3_F16;
   };
+  // The per-chunk steps take a compile-time flag (GEN / M0P): M0P compiles
+  // them for chunks known to hold M0 keys and values only, without the M3
+  // paths and their wave-uniform branches (the M0 chunks of pools that also
+  // hold M3 pages).
+  using GEN = std::false_type;
+  using M0P = std::true_type;
 
   // ---- loads of one chunk into registers ----
   // Buffer loads against a per-page resource (base = the blob, size = the
@@ -511,8 +517,9 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   constexpr int kNT = 2;  // cache policy: nontemporal (page bytes are read once per launch)
   // part 0: the whole chunk; 1: value pieces and all scales / biases;
   // 2: key codes or rows; 3: M0 key codes only; 4: M3 key rows only
-  auto load_part = [&](const PageMeta& m, auto& R, auto kbi, auto part) __attribute__((always_inline)) {
+  auto load_part = [&](const PageMeta& m, auto& R, auto kbi, auto part, auto m0) __attribute__((always_inline)) {
     constexpr int P = decltype(part)::value;
+    constexpr bool kM0 = decltype(m0)::value;
     const int c0 = m.c0;
     auto dma_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
       const uint32_t l = KMODE == KEYS_M3 ? 0u : fresh_lane();
@@ -557,7 +564,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       if constexpr (P == 0 || P == 2 || P == 4) dma_keys(m.krs);
     } else if constexpr (KMODE == KEYS_M0) {
       if constexpr (P != 4) word_keys(m.krs);
-    } else if (key_is_m3(m)) {  // one chunk in flight: a wave-uniform branch
+    } else if (!kM0 && key_is_m3(m)) {  // one chunk in flight: a wave-uniform branch
       if constexpr (P == 0 || P == 2 || P == 4) dma_keys(m.krs);
     } else {
       if constexpr (P != 4) word_keys(m.krs);
@@ -580,8 +587,8 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   using LP2 = std::integral_constant<int, 2>;
   using LP3 = std::integral_constant<int, 3>;
   using LP4 = std::integral_constant<int, 4>;
-  auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi) __attribute__((always_inline)) {
-    load_part(m, R, kbi, LP0{});
+  auto load_chunk = [&](const PageMeta& m, auto& R, auto kbi, auto m0) __attribute__((always_inline)) {
+    load_part(m, R, kbi, LP0{}, m0);
   };
 
   // ---- registers -> an LDS stage buffer: value codes in padded rows, scales as loaded ([32][G] fp16) ----
@@ -627,14 +634,15 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   };
 
   // ---- score of one chunk: logits of chunk tokens 8 kb + e for head r ----
-  auto score_chunk = [&](const PageMeta& m, const auto& R, const uint32_t* lds, auto kbi,
-                         float* Ls) __attribute__((always_inline)) {
+  auto score_chunk = [&](const PageMeta& m, const auto& R, const uint32_t* lds, auto kbi, float* Ls,
+                         auto m0) __attribute__((always_inline)) {
+    constexpr bool kM0 = decltype(m0)::value;
     const uint32_t* kl = kbuf(kbi);
     // MFMA results are read a few instructions after issue only at the very
     // end: the M3 paths keep four independent accumulation chains (token
     // tile hh x high / residual query part), the M0 path scales group g - 1
     // while the MFMAs of group g run
-    if (key_is_m3(m)) {
+    if (!kM0 && key_is_m3(m)) {
       if constexpr (kDmaK) {
         const uint32_t l3 = KMODE == KEYS_M3 ? 0u : fresh_lane();
         f32x4 dh[2], dl[2];
@@ -853,9 +861,10 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   // same overflow margin: weight x scale x 16 reaches fp16's maximum only
   // for 8-bit scales above 1023).  The epilogue divides by kVS.
   constexpr float kVS = VBITS == 8 ? 16.f : 1.f;
-  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa) __attribute__((always_inline)) {
+  auto mix_chunk = [&](const PageMeta& m, const uint32_t* lds, const float* pa, auto m0) __attribute__((always_inline)) {
+    constexpr bool kM0 = decltype(m0)::value;
     bool v_m0 = true;
-    if constexpr (VM3) v_m0 = is_m0(m.vfmt);
+    if constexpr (VM3 && !kM0) v_m0 = is_m0(m.vfmt);
     if (v_m0) {
       const bool v_affine = VAFF && m.vfmt == DC_FMT_M0_AFFINE;
       const float zp = v_affine ? 0.f : float((1 << (VBITS - 1)) - 1);
@@ -1085,7 +1094,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       const PageFields f = page_fields(np < 64 ? np : 64);
       const int nch0 = (__builtin_amdgcn_readlane(f.T, 0) + 31) >> 5;
       early = cb < (np == 1 && ce > 0 ? min(nch0, ce) : nch0);
-      if (early) load_chunk(lane_meta(f, 0, cb * 32), RA, KB0{});
+      if (early) load_chunk(lane_meta(f, 0, cb * 32), RA, KB0{}, GEN{});
     }
   }
 
@@ -1186,8 +1195,8 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       uint32_t* const buf1 = lds_all + Cfg::STAGE;
       PageMeta cur = chunk_meta(0);
       PageMeta nxt = total > 1 ? chunk_meta(1) : no_chunk(cur);
-      if (!(early && base == 0)) load_chunk(cur, RA, KB0{});  // (early: the same chunk, already issued)
-      load_chunk(nxt, RB, KB1{});
+      if (!(early && base == 0)) load_chunk(cur, RA, KB0{}, GEN{});  // (early: the same chunk, already issued)
+      load_chunk(nxt, RB, KB1{}, GEN{});
       prep_queries();
       float Ls[8], pa[8];
       stage_chunk(RA, buf0);
@@ -1198,23 +1207,23 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       // this block once the first chunk could be issued before the loop,
       // and the reads it hoisted above the stage then saw stale rows.
       if constexpr (kDmaK) asm volatile("" ::: "memory");
-      score_chunk(cur, RA, buf0, KB0{}, Ls);
+      score_chunk(cur, RA, buf0, KB0{}, Ls, GEN{});
       softmax_chunk(cur, Ls, pa);
       int j = 0;
       // chunk j: values in stage buffer bm (keys in km, already scored);
       // chunk j + 1: registers X, keys in ks; chunk j + 2 loads into Y, km
       auto step = [&](R_t& X, R_t& Y, uint32_t* bm, uint32_t* bs, auto km, auto ks) __attribute__((always_inline)) -> bool {
         if (j + 1 >= total) {  // last chunk: mix only
-          mix_chunk(cur, bm, pa);
+          mix_chunk(cur, bm, pa, GEN{});
           return false;
         }
         const PageMeta n2 = j + 2 < total ? chunk_meta(j + 2) : no_chunk(nxt);
-        load_chunk(n2, Y, km);
+        load_chunk(n2, Y, km, GEN{});
         float Ln[8];
         stage_chunk(X, bs);
         if constexpr (kDmaK) asm volatile("" ::: "memory");  // (as for the first chunk)
-        score_chunk(nxt, X, bs, ks, Ln);
-        mix_chunk(cur, bm, pa);
+        score_chunk(nxt, X, bs, ks, Ln, GEN{});
+        mix_chunk(cur, bm, pa, GEN{});
         softmax_chunk(nxt, Ln, pa);
         cur = nxt;
         nxt = n2;
@@ -1230,52 +1239,78 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       // issued before them: a chunk's M3 key and value rows are always
       // issued before its value pieces and scales (LP1), and the score and
       // the mix read the rows only after the stage.
-      R_t R, RN;
-      PageMeta cur = chunk_meta(0);
-      if constexpr (VM3)
-        if (!is_m0(cur.vfmt)) load_value_rows(cur);
-      load_chunk(cur, R, KB0{});  // (M3 key rows first, then the register loads)
-      prep_queries();
-      for (int j = 0; j < total; ++j) {
-        const PageMeta nm = j + 1 < total ? chunk_meta(j + 1) : no_chunk(cur);
-        float Ls[8], pa[8];
-        stage_chunk(R, lds_all);
-        // At one wave per SIMD the value pieces, scales and M0 key codes of
-        // chunk j + 1 go out as soon as this chunk is staged (the codes into
-        // a second set, copied over after the mix), and M3 key rows once
-        // this chunk is scored, its key buffer then being free (C5: 164.4 ->
-        // 162.6 us per launch for the values and scales, -> 161.6 us with
-        // the codes); with two waves per SIMD the other wave covers the
-        // wait, and the early values measured slower (C4: 40.7 -> 41.4 us).
-        // (a next chunk with M3 key or value rows, rare and wave-uniform,
-        // takes its register loads after those rows' DMA, at the end of the
-        // step; LP0 issues the key rows before the register loads)
-        const bool nm_vrows = VM3 && j + 1 < total && !is_m0(nm.vfmt);
-        const bool nm_rows = key_is_m3(nm) || nm_vrows;
-        if constexpr (kSplitReload) {
-          if (!nm_rows) load_part(nm, R, KB0{}, LP1{});
-          if constexpr (KMODE != KEYS_M3) load_part(nm, RN, KB0{}, LP3{});  // (an M3 key page loads none)
-        }
-        score_chunk(cur, R, lds_all, KB0{}, Ls);
-        if constexpr (kSplitReload)
-          load_part(nm, R, KB0{}, LP4{});
-        else if (!nm_vrows)
-          load_part(nm, R, KB0{}, LP0{});
-        softmax_chunk(cur, Ls, pa);
-        mix_chunk(cur, lds_all, pa);
-        if constexpr (VM3)
-          if (nm_vrows) load_value_rows(nm);
-        if constexpr (kSplitReload) {
-          if (nm_rows) load_part(nm, R, KB0{}, LP1{});
-        } else if (nm_vrows) {
-          load_part(nm, R, KB0{}, LP0{});
-        }
-        if constexpr (kSplitReload && KMODE != KEYS_M3)
+      // Chunks [j0, j1) of the batch; m0 = M0P where every one of them holds
+      // M0 keys and values.
+      auto walk = [&](auto m0, int j0, int j1) __attribute__((always_inline)) {
+        constexpr bool kM0 = decltype(m0)::value;
+        R_t R, RN;
+        PageMeta cur = chunk_meta(j0);
+        if constexpr (VM3 && !kM0)
+          if (!is_m0(cur.vfmt)) load_value_rows(cur);
+        load_chunk(cur, R, KB0{}, m0);  // (M3 key rows first, then the register loads)
+        prep_queries();
+        for (int j = j0; j < j1; ++j) {
+          const PageMeta nm = j + 1 < j1 ? chunk_meta(j + 1) : no_chunk(cur);
+          float Ls[8], pa[8];
+          stage_chunk(R, lds_all);
+          // At one wave per SIMD the value pieces, scales and M0 key codes of
+          // chunk j + 1 go out as soon as this chunk is staged (the codes into
+          // a second set, copied over after the mix), and M3 key rows once
+          // this chunk is scored, its key buffer then being free (C5: 164.4 ->
+          // 162.6 us per launch for the values and scales, -> 161.6 us with
+          // the codes); with two waves per SIMD the other wave covers the
+          // wait, and the early values measured slower (C4: 40.7 -> 41.4 us).
+          // (a next chunk with M3 key or value rows, rare and wave-uniform,
+          // takes its register loads after those rows' DMA, at the end of the
+          // step; LP0 issues the key rows before the register loads)
+          const bool nm_vrows = VM3 && !kM0 && j + 1 < j1 && !is_m0(nm.vfmt);
+          const bool nm_rows = (!kM0 && key_is_m3(nm)) || nm_vrows;
+          if constexpr (kSplitReload) {
+            if (!nm_rows) load_part(nm, R, KB0{}, LP1{}, m0);
+            if constexpr (KMODE != KEYS_M3) load_part(nm, RN, KB0{}, LP3{}, m0);  // (an M3 key page loads none)
+          }
+          score_chunk(cur, R, lds_all, KB0{}, Ls, m0);
+          if constexpr (kSplitReload)
+            load_part(nm, R, KB0{}, LP4{}, m0);
+          else if (!nm_vrows)
+            load_part(nm, R, KB0{}, LP0{}, m0);
+          softmax_chunk(cur, Ls, pa);
+          mix_chunk(cur, lds_all, pa, m0);
+          if constexpr (VM3 && !kM0)
+            if (nm_vrows) load_value_rows(nm);
+          if constexpr (kSplitReload) {
+            if (nm_rows) load_part(nm, R, KB0{}, LP1{}, m0);
+          } else if (nm_vrows) {
+            load_part(nm, R, KB0{}, LP0{}, m0);
+          }
+          if constexpr (kSplitReload && KMODE != KEYS_M3)
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh)
+            for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-            for (int i = 0; i < Cfg::KG * (KBITS / 4); ++i) R.kw[hh][i] = RN.kw[hh][i];
-        cur = nm;
+              for (int i = 0; i < Cfg::KG * (KBITS / 4); ++i) R.kw[hh][i] = RN.kw[hh][i];
+          cur = nm;
+        }
+      };
+      if constexpr ((KMODE == KEYS_MIXED || VM3) && waves_per_simd<HD, KMODE, KBITS, VBITS, NQB>() == 1) {
+        // Pools that may hold M3 pages (one wave per SIMD): the batch's
+        // chunks before its first page with M3 keys or values take the
+        // M0-only walk.  Its per-chunk code has none of the M3 branches: on
+        // C5 about 150 fewer scalar and 90 fewer vector instructions per
+        // chunk, and 161.6 -> 154.0 us per launch.  (Built for two waves per
+        // SIMD, the instances with two walks spill.)
+        const bool m3p = lane < nb && cnt > 0 && (kf == DC_FMT_M3_F16 || !is_m0(vf));
+        const uint64_t m3b = __ballot(m3p);
+        int jm3 = total;
+        if (m3b != 0) {
+          const int i0 = int(__builtin_ctzll(m3b));
+          jm3 = fast ? max((i0 << cps) - off, 0) : __builtin_amdgcn_readlane(cbeg, i0);
+        }
+        if (jm3 > 0) walk(M0P{}, 0, jm3);
+        if (jm3 < total) walk(GEN{}, jm3, total);
+      } else if constexpr (KMODE == KEYS_M0 && !VM3) {
+        walk(M0P{}, 0, total);
+      } else {
+        walk(GEN{}, 0, total);
       }
     }
   }

@@ -304,13 +304,21 @@ class PageRecords:
     (``dc_gather_page_records``), so the MFMA kernel's waves skip the
     page-table and descriptor reads before their first page loads.  A
     snapshot of the plan, both tables and both pools' descriptors: stale,
-    and refused by :func:`decode_paged`, once any of them changes."""
+    and refused by :func:`decode_paged`, once any of them changes.  It also
+    holds the formats of the pages the tables reference (``k_mask`` /
+    ``v_mask``, ``dc_pool.format_mask`` bits), which :func:`decode_paged`
+    passes in place of the pools' masks: the launcher then picks the kernel
+    instance for the formats this launch meets (a layer whose key pages are
+    all M0 runs the M0-only instance although the pool also holds fp16
+    key pages of other layers)."""
 
     data: object     # device uint8 tensor: n_items x stride x 16 bytes
     stride: int      # records per item (items with more pages read the tables)
     plan: DecodePlan
     sources: tuple   # (k_table, v_table, key pool, value pool), held so their identities stay unique
     versions: tuple  # the tables' and pools' versions at gather time
+    k_mask: int = -1  # formats of the referenced key / value pages (-1: the pools' masks)
+    v_mask: int = -1
 
     @staticmethod
     def versions_of(k_table, v_table, pool, vpool) -> tuple:
@@ -342,8 +350,14 @@ def gather_records(pool: DevicePagePool, k_table, v_table, seq_pages, plan: Deco
                                            plan.n_items, B, H, C.c_void_p(data.data_ptr()), rs,
                                            C.c_void_p(current_stream_ptr()))
     _lib.check(st, "dc_gather_page_records")
+    # the formats of every page the plan reads (pages [0, seq_pages[b]) of
+    # every row)
+    kt, vt = k_table.cpu().numpy(), v_table.cpu().numpy()
+    live = np.broadcast_to(np.arange(stride_t)[None, None, :] < sp[:, None, None], kt.shape)
+    k_mask = pool.format_mask_of(kt[live]) & pool.format_mask
+    v_mask = vpool.format_mask_of(vt[live]) & vpool.format_mask
     return PageRecords(data, rs, plan, (k_table, v_table, pool, vpool),
-                       PageRecords.versions_of(k_table, v_table, pool, vpool))
+                       PageRecords.versions_of(k_table, v_table, pool, vpool), k_mask, v_mask)
 
 
 def workspace_bytes(plan: DecodePlan, n_q: int, head_dim: int) -> int:
@@ -424,7 +438,11 @@ def decode_paged(
     need = workspace_bytes(plan, Q, hd)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=queries.device)
-    args = (pool.c_pool(), vpool.c_pool(), C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
+    kp, vp = pool.c_pool(), vpool.c_pool()
+    if records is not None and records.k_mask > 0 and records.v_mask > 0:
+        # (checked fresh below: the masks are those of these tables' pages)
+        kp.format_mask, vp.format_mask = records.k_mask, records.v_mask
+    args = (kp, vp, C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
             C.c_void_p(plan.items.data_ptr()), plan.n_items,
             C.c_void_p(plan.merges.data_ptr() if plan.merges is not None and merge else 0),
             plan.n_merges if merge else 0, C.c_void_p(queries.data_ptr()), dtype_code(queries), float(query_scale),

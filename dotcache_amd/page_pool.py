@@ -221,6 +221,18 @@ class DevicePagePool:
     def tokens_of(self, page_ids) -> np.ndarray:
         return self._host_desc["tokens"][np.asarray(page_ids, dtype=np.int64)].astype(np.int64)
 
+    def format_mask_of(self, page_ids) -> int:
+        """``dc_pool.format_mask`` bits of the formats these pages hold (a
+        subset of :attr:`format_mask`)."""
+        ids = np.unique(np.asarray(page_ids, dtype=np.int64).ravel())
+        if ids.size == 0:
+            return 0
+        d = self._host_desc[ids]
+        mask = 0
+        for fmt, bits in set(zip(d["format"].tolist(), d["bits"].tolist())):
+            mask |= _lib.format_bit(int(fmt), int(bits))
+        return mask
+
     def validate_ids(self, page_ids) -> None:
         ids = np.asarray(page_ids, dtype=np.int64).ravel()
         if ids.size and (ids.min() < 0 or ids.max() >= self._n_pages or not self._live[ids].all()):

@@ -246,3 +246,38 @@ def test_page_records_give_the_same_outputs(kfmt, vfmt, vgs, hd, Q, tpp):
     case["kpool"].set_tokens([pid], case["kpool"].tokens_of([pid]))
     with pytest.raises(ValueError):
         decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"], records=rec)
+
+
+def test_page_records_narrow_the_format_mask():
+    """Page records carry the formats of the pages their tables reference.
+    A batch whose key pages are all M0, in a pool that also holds fp16 key
+    pages of another batch, then runs the M0-only kernel instance: within
+    1e-4 of the mixed-format instance (which it gets without records; two
+    instances need not round alike) and within the bound of the oracle; the
+    other batch keeps the fp16 bit."""
+    from dotcache_amd import _lib
+    from dotcache_amd.decode import chunks_per_page, decode_paged, gather_records, make_plan
+
+    rng = np.random.default_rng(808)
+    vfmt = dict(bits=8, scheme="symmetric")
+    m0 = _case(rng, [64 * 9 - 5, 64 * 30 + 1, 33], 128, 6, 64, dict(bits=4), vfmt, 64)
+    m3 = _case(rng, [64 * 5, 70], 128, 6, 64, dict(mode="M3"), vfmt, 64)
+    pool = m0["kpool"]
+    assert m3["kpool"] is pool and m3["vpool"] is m0["vpool"], "both batches share the pools"
+    m3_bit = _lib.format_bit(_lib.FMT_M3_F16, 0)
+    assert pool.format_mask & m3_bit
+    cpp = chunks_per_page(pool.geometry.page_capacity)
+    for case, has_m3 in ((m0, False), (m3, True)):
+        counts = case["counts"]
+        args = (pool, case["kt"], case["vt"], counts)
+        plan = make_plan(counts, 1, device="cuda", target_items=11, chunks_per_page=cpp)
+        rec = gather_records(*args, plan, v_pool=case["vpool"])
+        assert rec.k_mask != 0 and (rec.k_mask & ~pool.format_mask) == 0
+        assert bool(rec.k_mask & m3_bit) == has_m3
+        assert rec.v_mask == case["vpool"].format_mask
+        want = decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"]).clone()
+        got = decode_paged(*args, case["q"], plan=plan, v_pool=case["vpool"], records=rec)
+        diff = float((got - want).abs().max().item())
+        assert diff < 1e-4, f"fp16 keys {has_m3}: records against tables, max diff {diff}"
+        err = float(np.max(np.abs(got.cpu().numpy()[:, 0] - case["want"])))
+        assert err < KERNEL_TOL, f"fp16 keys {has_m3}: max-abs error {err}"
