@@ -157,11 +157,18 @@ struct MfmaCfg {
 // two unpipelined waves per SIMD (at most 256 registers each) hide each
 // other's waits, where one pipelined wave cannot (C4: 42.1 against 49.3 us
 // per launch).  Pools of M3 keys (C3) stream bytes and keep one pipelined
-// wave (two waves: 32.9 against 32.7 us).
+// wave (two waves: 32.9 against 32.7 us).  At head_dim 256 (M0 keys and
+// values, 4-bit, blocks of 4 heads) the same holds once the key codes
+// come by DMA: 133.1 against 156.1 us per launch on C5's pages without the
+// fp16 window (the M0 pool, paired replays).
 template <int HD, int KMODE, int KBITS, int VBITS, int NQB>
 constexpr int waves_per_simd() {
-  // (8-bit keys and values with 8 heads per block spill at 256 registers)
-  return HD == 128 && KMODE != KEYS_M3 && NQB <= 8 && !(KBITS == 8 && VBITS == 8 && NQB == 8) ? 2 : 1;
+  // (8-bit keys and values with 8 heads per block, and head_dim 256 with 8,
+  // spill at 256 registers)
+  return (HD == 128 && KMODE != KEYS_M3 && NQB <= 8 && !(KBITS == 8 && VBITS == 8 && NQB == 8)) ||
+                 (HD == 256 && KMODE == KEYS_M0 && KBITS == 4 && VBITS == 4 && NQB == 4)
+             ? 2
+             : 1;
 }
 
 // Two staged chunks in flight where the registers allow it: one wave per
@@ -172,12 +179,13 @@ constexpr bool pipelined() {
 }
 
 // Registers one chunk needs from HBM: this lane's KW words of each M0 key
-// code block (M3 key rows go straight to LDS), the value code pieces and
-// the scale / bias words.
-template <int HD, int VGS, int VBITS, int KMODE, int KBITS>
+// code block (KWREG: pipelined instances; the others take M0 codes and M3
+// key rows straight to LDS), the value code pieces and the scale / bias
+// words.
+template <int HD, int VGS, int VBITS, int KMODE, int KBITS, bool KWREG = true>
 struct ChunkRegs {
   using Cfg = MfmaCfg<HD, VGS, VBITS>;
-  static constexpr bool kKeyWords = KMODE != KEYS_M3;
+  static constexpr bool kKeyWords = KMODE != KEYS_M3 && KWREG;
   static constexpr int KW = KBITS / 4;  // code words of one lane's 8 channels
   uint32_t kw[kKeyWords ? 2 : 1][kKeyWords ? Cfg::KG * KW : 1];
   u32x4 vr[Cfg::NVP];  // value code pieces, blob byte order
@@ -252,6 +260,31 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   };
   using KB0 = std::integral_constant<int, 0>;
   using KB1 = std::integral_constant<int, 1>;
+  // M0 key codes of the unpipelined instances go to LDS by DMA too: 16-byte
+  // loads, each instruction 1 KiB of two (4-bit) or one (8-bit) groups'
+  // code blocks, contiguous in HBM.  In registers (a 4-byte load per group
+  // and tile: four 64-byte pieces of two cache lines per instruction) the
+  // same bytes cost the memory system far more: the C5 kernel with its
+  // arithmetic left out took 139 us per launch with those loads and 117 us
+  // with 16-byte ones.  Layout [group][slot][KBLK bytes]: chunk token t at
+  // slot 16 hh + m, its row m of tile hh (t = 8 (m / 4) + 4 hh + m % 4), so
+  // the 64 words one score read takes (16 rows x 4 lanes) are contiguous.
+  // Slot 0 shares kbuf0 with the M3 key rows (a chunk holds one or the
+  // other); the one-wave M0 walk double-buffers into slot 1 (vbuf, which M0
+  // chunks leave unused, or a buffer of its own).
+  constexpr bool kDmaM0 = KMODE != KEYS_M3 && !kPipe;
+  constexpr bool kM0Two = kDmaM0 && waves_per_simd<HD, KMODE, KBITS, VBITS, NQB>() == 1;
+  constexpr int KCW = 8 * Cfg::KG * KBLK;  // words of one chunk's key codes
+  static_assert(KCW <= 16 * HD, "a chunk's M0 codes fit the M3 row buffers");
+  __shared__ __attribute__((aligned(16))) uint32_t kcb0[kDmaM0 && !kDmaK ? KCW : 1];
+  __shared__ __attribute__((aligned(16))) uint32_t kcb1[kM0Two && !VM3 ? KCW : 1];
+  auto kcode = [&](auto bi) -> uint32_t* {
+    if constexpr (decltype(bi)::value == 0) {
+      if constexpr (kDmaK) return kbuf0; else return kcb0;
+    } else {
+      if constexpr (VM3) return vbuf; else return kcb1;
+    }
+  };
 
   // The kernel arguments the prologue uses, read in one round of scalar
   // loads at entry.  Read where each is first used, they were waited for one
@@ -467,6 +500,20 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
   uint32_t koff_m0[2];
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) koff_m0[hh] = (8 * (r >> 2) + 4 * hh + (r & 3)) * KBLK + KBITS * kb;
+  // M0 code DMA: lane l of instruction i fetches 16-byte piece pc of the
+  // code block of group GPI i + gl, chunk token t of slot s (gl = l / (32
+  // NPC), s = (l % (32 NPC)) / NPC, pc = l % NPC): the lane's part of the
+  // source offset is fixed for the item, the instruction's part (GPI i
+  // groups) wave-uniform.  kcrd: this lane's score read, slot r of tile 0,
+  // word kb KBITS / 4.
+  constexpr int NPC = KBLK / 16, GPI = 2 / NPC, NKD = KG / GPI;
+  uint32_t kcsrc = 0, kcrd = 0;
+  if constexpr (kDmaM0) {
+    const uint32_t l = uint32_t(lane), gl = l / (32 * NPC), sl = (l % (32 * NPC)) / NPC, pc = l % NPC;
+    const uint32_t t = 8 * ((sl & 15) >> 2) + 4 * (sl >> 4) + (sl & 3);
+    kcsrc = gl * uint32_t(CAP * KBLK) + t * KBLK + 16 * pc;
+    kcrd = uint32_t(r * (KBLK / 4) + kb * (KBITS / 4));
+  }
   // key DMA: rows of PPR pieces, RPI rows per instruction, NDMA instructions
   // per chunk; instruction i writes rows RPI i .. RPI i + RPI - 1, lane l slot
   // l % PPR of row RPI i + l / PPR, from source piece (l % PPR) ^ key_swz(row).
@@ -534,7 +581,15 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       }
     };
     auto word_keys = [&](__amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
-      if constexpr (P == 0 || P == 2 || P == 3)
+      if constexpr ((P == 0 || P == 2 || P == 3) && kDmaM0) {
+#pragma unroll
+        for (int i = 0; i < NKD; ++i) {
+          // (plain variables for the offsets, as in dma_keys)
+          const int soff = c0 * KBLK + i * GPI * CAP * KBLK;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(kcode(kbi) + 256 * i),
+                                                   16, kcsrc, soff, 0, kNT);
+        }
+      } else if constexpr (P == 0 || P == 2 || P == 3)
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
@@ -765,7 +820,11 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             if constexpr (KBITS == 4) {
-              const uint32_t w = R.kw[hh][g];
+              uint32_t w;
+              if constexpr (kDmaM0)
+                w = kcode(kbi)[kcrd + g * 8 * KBLK + hh * 4 * KBLK];
+              else
+                w = R.kw[hh][g];
               // nibble i of the word is channel i; channels i and i + 4 sit 16
               // bits apart, so one mask and the fp16 magic 0x6400 give the pair
               // (1024 + n_i, 1024 + n_{i+4}) (nibbles 0, 2) or 16 x that offset
@@ -780,7 +839,15 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
               // bytes (2j, 2j + 1) under the magic's 0x64 bytes, giving the
               // pair (1024 + n_2j, 1024 + n_2j+1), and one packed add makes
               // it n - zp exactly (|n - zp| <= 255 is exact in fp16)
-              const uint32_t wa = R.kw[hh][2 * g], wb = R.kw[hh][2 * g + 1];
+              uint32_t wa, wb;
+              if constexpr (kDmaM0) {
+                const uint32_t* kc = kcode(kbi) + kcrd + g * 8 * KBLK + hh * 4 * KBLK;
+                wa = kc[0];
+                wb = kc[1];
+              } else {
+                wa = R.kw[hh][2 * g];
+                wb = R.kw[hh][2 * g + 1];
+              }
               ka[hh].u[0] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05010500u)) + kadd0);
               ka[hh].u[1] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wa, 0x05030502u)) + kadd0);
               ka[hh].u[2] = bits_of(h2_of(__builtin_amdgcn_perm(fp16_magic, wb, 0x05010500u)) + kadd0);
@@ -1076,7 +1143,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
     m.c0 = c0;
     return m;
   };
-  using R_t = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS>;
+  using R_t = ChunkRegs<HD, VGS, VBITS, KMODE, KBITS, !kDmaM0>;
   R_t RA, RB;  // the pipeline's register sets
   // Pipelined instances with DMA keys issue the item's first chunk straight
   // from page 0's descriptors, before the batch layout (its prefix sum, the
@@ -1243,8 +1310,45 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
       // M0 keys and values.
       auto walk = [&](auto m0, int j0, int j1) __attribute__((always_inline)) {
         constexpr bool kM0 = decltype(m0)::value;
+        if constexpr (kM0 && kM0Two) {
+          // M0 chunks at one wave per SIMD: the codes double-buffered, so
+          // chunk j + 1's go out right after chunk j is staged, into the
+          // other slot, before its value pieces and scales, whose wait at
+          // the next stage then covers the codes too (vector memory loads
+          // complete in issue order).  Two steps per pass: each slot is a
+          // fixed LDS object.
+          R_t R;
+          PageMeta cur = chunk_meta(j0);
+          load_chunk(cur, R, KB0{}, m0);
+          prep_queries();
+          int j = j0;
+          auto step = [&](auto ks, auto kn) __attribute__((always_inline)) -> bool {
+            const PageMeta nm = j + 1 < j1 ? chunk_meta(j + 1) : no_chunk(cur);
+            float Ls[8], pa[8];
+            stage_chunk(R, lds_all);
+            asm volatile("" ::: "memory");  // (the codes of slot ks are read only after the stage)
+            load_part(nm, R, kn, LP3{}, m0);
+            load_part(nm, R, kn, LP1{}, m0);
+            score_chunk(cur, R, lds_all, ks, Ls, m0);
+            softmax_chunk(cur, Ls, pa);
+            mix_chunk(cur, lds_all, pa, m0);
+            cur = nm;
+            return ++j < j1;
+          };
+          while (step(KB0{}, KB1{}) && step(KB1{}, KB0{})) {
+          }
+          return;
+        }
         R_t R, RN;
         PageMeta cur = chunk_meta(j0);
+        // The compiler does not order an LDS DMA (buffer_load ... lds) after
+        // earlier reads of the same buffer: it moved a next chunk's key DMA
+        // in between the score's reads of the codes it overwrote.  Asm
+        // statements with a memory clobber keep every DMA below the reads of
+        // its buffer, and wait for those reads (lgkmcnt) before it: here
+        // (after the other walk's last reads), after the score (key buffer)
+        // and after the mix (value row buffer).
+        asm volatile("" ::: "memory");
         if constexpr (VM3 && !kM0)
           if (!is_m0(cur.vfmt)) load_value_rows(cur);
         load_chunk(cur, R, KB0{}, m0);  // (M3 key rows first, then the register loads)
@@ -1264,18 +1368,25 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
           // takes its register loads after those rows' DMA, at the end of the
           // step; LP0 issues the key rows before the register loads)
           const bool nm_vrows = VM3 && !kM0 && j + 1 < j1 && !is_m0(nm.vfmt);
-          const bool nm_rows = (!kM0 && key_is_m3(nm)) || nm_vrows;
+          // (with M0 codes by DMA every chunk's keys come as rows: after the
+          // score, which frees slot 0, and before the register loads)
+          const bool nm_rows = kDmaM0 || (!kM0 && key_is_m3(nm)) || nm_vrows;
           if constexpr (kSplitReload) {
             if (!nm_rows) load_part(nm, R, KB0{}, LP1{}, m0);
-            if constexpr (KMODE != KEYS_M3) load_part(nm, RN, KB0{}, LP3{}, m0);  // (an M3 key page loads none)
+            if constexpr (KMODE != KEYS_M3 && !kDmaM0)
+              load_part(nm, RN, KB0{}, LP3{}, m0);  // (an M3 key page loads none)
           }
           score_chunk(cur, R, lds_all, KB0{}, Ls, m0);
-          if constexpr (kSplitReload)
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if constexpr (kSplitReload && kDmaM0)
+            load_part(nm, R, KB0{}, LP2{}, m0);
+          else if constexpr (kSplitReload)
             load_part(nm, R, KB0{}, LP4{}, m0);
           else if (!nm_vrows)
             load_part(nm, R, KB0{}, LP0{}, m0);
           softmax_chunk(cur, Ls, pa);
           mix_chunk(cur, lds_all, pa, m0);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           if constexpr (VM3 && !kM0)
             if (nm_vrows) load_value_rows(nm);
           if constexpr (kSplitReload) {
@@ -1283,7 +1394,7 @@ __global__ void __launch_bounds__(64, (waves_per_simd<HD, KMODE, KBITS, VBITS, N
           } else if (nm_vrows) {
             load_part(nm, R, KB0{}, LP0{}, m0);
           }
-          if constexpr (kSplitReload && KMODE != KEYS_M3)
+          if constexpr (kSplitReload && KMODE != KEYS_M3 && !kDmaM0)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
