@@ -53,6 +53,9 @@ def parse():
                          "configuration's own line)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from Python each step instead of replaying captured HIP graphs")
+    ap.add_argument("--one-launch", action="store_true",
+                    help="run an exact recent window (c5) in the same decode launch as the 4-bit pages instead of "
+                         "a launch of its own")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--shortlist-pages", type=int, default=0, metavar="N",
                     help="only time the execution shortlist kernels: relevance of N pages (4-row sketches, "
@@ -373,7 +376,8 @@ def main():
     set_decode_path(args.decode_path)
     set_mfma_head_block(args.head_block)
     wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
-                        scatter_pages=not args.contiguous_pages, key_bits=args.key_bits)
+                        scatter_pages=not args.contiguous_pages, key_bits=args.key_bits,
+                        window_launch=not args.one_launch)
     spec = wl.spec
     # "fill": per-layer plans of a launch's item budget cut at 32-token chunks
     # by page cost; "pages": --pages-per-split whole-page splits
@@ -531,6 +535,7 @@ def main():
             "plan": plan_kind,
             "page_records": bool(wl.records),
             "pages_per_split": wl.plan.pages_per_split,
+            "decode_launches_per_layer": 2 if wl.plan.n_front else 1,
             "launch": "eager" if args.eager else "hip graph of the whole step",
             "parallelism": "single GPU",
         },
@@ -547,7 +552,8 @@ def main():
             "traffic": profiled_traffic(spec.name, plan_kind, wl.plan.pages_per_split, args.decode_path,
                                         args.head_block),
             "kernel": ("decode_generic_kernel" if args.decode_path == "generic" else "decode_mfma_kernel")
-                      + " (dc_decode_paged, one launch per layer)",
+                      + (" (dc_decode_paged: the exact window's launch, then the rest's; launch_us is both)"
+                         if wl.plan.n_front else " (dc_decode_paged, one launch per layer)"),
             "launch_us": launch_ms * 1e3,
             "launch_us_stat": f"mean over {n_med} replays of one step's {L} decode launches (event per replay)",
             "launch_us_median": float(np.median(dec_ms)) * 1e3,

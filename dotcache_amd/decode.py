@@ -62,6 +62,10 @@ class DecodePlan:
     checked: set = None               # (seq_pages, n_kv_heads, table_stride) keys already validated
     chunks_per_page: int = 1          # the page split granularity the items were cut for
     largest_chunks: int = 0           # largest item in 32-token chunks (fill plans)
+    # items [0, n_front) run in a launch of their own ahead of the rest
+    # (make_region_plan: the pages of a different format mix, such as an
+    # exact recent window, kept out of the bulk launch's kernel instance)
+    n_front: int = 0
 
     def check(self, seq_pages: np.ndarray, n_kv_heads: int, table_stride: int, chunks_per_page: int = 1) -> None:
         """Raise ValueError unless every work item and merge item of the plan
@@ -124,17 +128,26 @@ def default_target_items() -> int:
     return DEFAULT_TARGET_ITEMS
 
 
-def waves_per_simd(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q: int) -> int:
+def waves_per_simd(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q: int, k_mask: int | None = None,
+                   v_mask: int | None = None) -> int:
     """Work items per SIMD the decode kernel for these pools and ``n_q``
-    runs at once (``dc_decode_waves_per_simd``): 1 or 2."""
+    runs at once (``dc_decode_waves_per_simd``): 1 or 2.  ``k_mask`` /
+    ``v_mask``: the formats of the pages the launch reads
+    (``format_mask_of``), when narrower than the pools'."""
     vpool = pool if v_pool is None else v_pool
-    return int(_lib.lib().dc_decode_waves_per_simd(pool.c_pool(), vpool.c_pool(), int(n_q)))
+    kp, vp = pool.c_pool(), vpool.c_pool()
+    if k_mask:
+        kp.format_mask = int(k_mask) & pool.format_mask
+    if v_mask:
+        vp.format_mask = int(v_mask) & vpool.format_mask
+    return int(_lib.lib().dc_decode_waves_per_simd(kp, vp, int(n_q)))
 
 
-def launch_target_items(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q: int) -> int:
+def launch_target_items(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q: int, k_mask: int | None = None,
+                        v_mask: int | None = None) -> int:
     """Items that fill one launch round: one per SIMD times the kernel's
     waves per SIMD."""
-    return default_target_items() * waves_per_simd(pool, v_pool, n_q)
+    return default_target_items() * waves_per_simd(pool, v_pool, n_q, k_mask, v_mask)
 
 
 def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items: int | None = None) -> int:
@@ -275,6 +288,125 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     return plan
 
 
+def _fill_units(unit_pages: np.ndarray, unit_last: np.ndarray, unit_cost, cpp: int, target: int,
+                min_chunks: int) -> tuple[np.ndarray, int]:
+    """``dc_plan_decode_fill`` over independent page runs ("units", each
+    planned as a sequence of one KV head): host items ``[n, 8]`` with the
+    unit index in the sequence field, and the largest item in chunks."""
+    L = _lib.lib()
+    ni, nm, npart, big = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
+    sp = np.ascontiguousarray(unit_pages, dtype=np.int32)
+    last = np.ascontiguousarray(unit_last, dtype=np.int32)
+    cost = None if unit_cost is None else np.ascontiguousarray(unit_cost, dtype=np.float32)
+
+    def plan(items_p, max_items, merges_p, max_merges):
+        return L.dc_plan_decode_fill(sp.ctypes.data, last.ctypes.data, sp.size, 1, cpp,
+                                     None if cost is None else cost.ctypes.data,
+                                     0 if cost is None else cost.shape[2], max(int(target), 1), int(min_chunks),
+                                     items_p, max_items, C.byref(ni), merges_p, max_merges, C.byref(nm),
+                                     C.byref(npart), C.byref(big))
+
+    st = plan(None, 0, None, 0)
+    if st not in (_lib.DC_OK, _lib.DC_ESPACE):
+        _lib.check(st, "dc_plan_decode_fill")
+    items = (_lib.WorkItem * max(ni.value, 1))()
+    merges = (_lib.MergeItem * max(nm.value, 1))()
+    _lib.check(plan(C.addressof(items), ni.value, C.addressof(merges), nm.value), "dc_plan_decode_fill")
+    return np.frombuffer(bytes(items), dtype=np.int32).reshape(-1, 8)[: ni.value].copy(), int(big.value)
+
+
+def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks_per_page: int = 1, page_cost=None,
+                     last_page_tokens=None, target_items: int | None = None, front_items: int | None = None,
+                     front_min_chunks: int = 1) -> DecodePlan:
+    """A fill plan in two launches: pages ``[front[b, 0], front[b, 1])`` of
+    every stream of sequence b (``front``: int ``[n_seqs, 2]``, an empty
+    range for none) are cut into ``front_items`` items (default: one per
+    32-token chunk) that run first, in a launch of their own; the pages
+    before and after that range into ``target_items`` items of near-equal
+    cost (as :func:`make_plan`), the second launch.  One merge per stream
+    then combines the partials of both.  Each launch takes the kernel
+    instance of the page formats its own items read, so a stream's few
+    pages of another format (an exact fp16 recent window among 4-bit
+    pages) do not hold the bulk launch to the instance that reads both
+    (``decode_paged``, with page records).  Arguments otherwise as for
+    :func:`make_plan` (fill plans only)."""
+    torch = _torch()
+    sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
+    if sp.ndim != 1 or sp.size == 0 or np.any(sp <= 0):
+        raise ValueError("seq_pages must be a non-empty 1-D array of positive page counts")
+    B, H = sp.size, int(n_kv_heads)
+    fr = np.asarray(front, dtype=np.int64).reshape(B, 2)
+    if np.any(fr[:, 0] < 0) or np.any(fr[:, 1] < fr[:, 0]) or np.any(fr[:, 1] > sp):
+        raise ValueError("front ranges must satisfy 0 <= begin <= end <= seq_pages")
+    cpp = max(int(chunks_per_page), 1)
+    full = 32 * cpp
+    last = np.full(B, full, dtype=np.int32) if last_page_tokens is None else np.asarray(last_page_tokens, np.int32)
+    if last.shape != (B,):
+        raise ValueError("last_page_tokens must have one entry per sequence")
+    cost = None if page_cost is None else np.asarray(page_cost, dtype=np.float32)
+    if cost is not None and (cost.ndim != 3 or cost.shape[:2] != (B, H) or cost.shape[2] < int(sp.max())):
+        raise ValueError("page_cost must have shape [n_seqs, n_kv_heads, >= max pages]")
+    target = int(target_items) if target_items else default_target_items()
+    key = ("region", sp.tobytes(), H, fr.tobytes(), cpp, None if cost is None else cost.tobytes(), last.tobytes(),
+           target, front_items, int(front_min_chunks), str(device))
+    hit = _plan_cache.get(key)
+    if hit is not None:
+        return hit
+
+    def plan_units(units, n_target, min_chunks):
+        """units: (b, h, p0, p1) page runs -> host items with real (seq,
+        head, pages), or an empty array."""
+        if not units:
+            return np.zeros((0, 8), dtype=np.int32), 0
+        u = np.asarray(units, dtype=np.int64)
+        pages = (u[:, 3] - u[:, 2]).astype(np.int32)
+        ulast = np.where(u[:, 3] == sp[u[:, 0]], last[u[:, 0]], full).astype(np.int32)
+        ucost = None
+        if cost is not None:
+            ucost = np.zeros((len(u), 1, int(pages.max())), dtype=np.float32)
+            for i, (b, h, p0, p1) in enumerate(u):
+                ucost[i, 0, : p1 - p0] = cost[b, h, p0:p1]
+        it, big = _fill_units(pages, ulast, ucost, cpp, n_target, min_chunks)
+        src = u[it[:, 0]]
+        it[:, 0], it[:, 1] = src[:, 0], src[:, 1]
+        it[:, 2] += src[:, 2].astype(np.int32)
+        it[:, 3] += src[:, 2].astype(np.int32)
+        return it, big
+
+    front_units = [(b, h, int(fr[b, 0]), int(fr[b, 1])) for b in range(B) for h in range(H) if fr[b, 1] > fr[b, 0]]
+    bulk_units = [(b, h, p0, p1) for b in range(B) for h in range(H)
+                  for p0, p1 in ((0, int(fr[b, 0])), (int(fr[b, 1]), int(sp[b]))) if p1 > p0]
+    if front_items is None:  # one item per chunk that holds tokens
+        front_items = sum((p1 - p0 - 1) * cpp + (min(cpp, (int(last[b]) + 31) // 32) if p1 == sp[b] else cpp)
+                          for b, h, p0, p1 in front_units)
+    f_it, f_big = plan_units(front_units, int(front_items), int(front_min_chunks))
+    b_it, b_big = plan_units(bulk_units, target, MIN_CHUNKS_PER_SPLIT)
+    items = np.concatenate([f_it, b_it]) if len(f_it) else b_it
+    # partial slots: every stream's items (front and bulk) take consecutive
+    # slots, merged by one merge item; a stream of one item writes its output
+    stream = items[:, 0].astype(np.int64) * H + items[:, 1]
+    merges, n_part = [], 0
+    for s in np.unique(stream):
+        rows = np.flatnonzero(stream == s)
+        if len(rows) == 1:
+            items[rows[0], 4] = -1
+            continue
+        items[rows, 4] = n_part + np.arange(len(rows), dtype=np.int32)
+        merges.append((int(s) // H, int(s) % H, n_part, len(rows)))
+        n_part += len(rows)
+    items[:, 7] = 0
+    host_merges = np.asarray(merges, dtype=np.int32).reshape(-1, 4)
+    dev_items = torch.from_numpy(items.ravel().view(np.uint8).copy()).to(device)
+    dev_merges = torch.from_numpy(host_merges.ravel().view(np.uint8).copy()).to(device) if len(merges) else None
+    big = max(f_big, b_big)
+    plan = DecodePlan(dev_items, dev_merges, len(items), len(merges), n_part, -(-big // cpp), items, host_merges,
+                      chunks_per_page=cpp, largest_chunks=big, n_front=len(f_it))
+    if len(_plan_cache) > 256:
+        _plan_cache.clear()
+    _plan_cache[key] = plan
+    return plan
+
+
 _PATHS = {"auto": 0, "generic": 1, "mfma": 2}
 
 
@@ -319,6 +451,10 @@ class PageRecords:
     versions: tuple  # the tables' and pools' versions at gather time
     k_mask: int = -1  # formats of the referenced key / value pages (-1: the pools' masks)
     v_mask: int = -1
+    # region plans (n_front > 0): k_mask / v_mask cover the bulk items'
+    # pages, these the front items'
+    front_k_mask: int = -1
+    front_v_mask: int = -1
 
     @staticmethod
     def versions_of(k_table, v_table, pool, vpool) -> tuple:
@@ -351,13 +487,30 @@ def gather_records(pool: DevicePagePool, k_table, v_table, seq_pages, plan: Deco
                                            C.c_void_p(current_stream_ptr()))
     _lib.check(st, "dc_gather_page_records")
     # the formats of every page the plan reads (pages [0, seq_pages[b]) of
-    # every row)
+    # every row; per launch for region plans)
     kt, vt = k_table.cpu().numpy(), v_table.cpu().numpy()
-    live = np.broadcast_to(np.arange(stride_t)[None, None, :] < sp[:, None, None], kt.shape)
-    k_mask = pool.format_mask_of(kt[live]) & pool.format_mask
-    v_mask = vpool.format_mask_of(vt[live]) & vpool.format_mask
+    if plan.n_front:
+        (fk, fv), (k_mask, v_mask) = (items_format_masks(pool, vpool, kt, vt, part)
+                                      for part in (it[: plan.n_front], it[plan.n_front:]))
+    else:
+        live = np.broadcast_to(np.arange(stride_t)[None, None, :] < sp[:, None, None], kt.shape)
+        k_mask = pool.format_mask_of(kt[live]) & pool.format_mask
+        v_mask = vpool.format_mask_of(vt[live]) & vpool.format_mask
+        fk = fv = -1
     return PageRecords(data, rs, plan, (k_table, v_table, pool, vpool),
-                       PageRecords.versions_of(k_table, v_table, pool, vpool), k_mask, v_mask)
+                       PageRecords.versions_of(k_table, v_table, pool, vpool), k_mask, v_mask, fk, fv)
+
+
+def items_format_masks(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray,
+                       items: np.ndarray) -> tuple[int, int]:
+    """``format_mask`` bits of the key and value pages these host work
+    items (``[n, 8]``) read from host tables ``kt`` / ``vt``."""
+    used = np.zeros(kt.shape, dtype=bool)
+    for seq, head, pb, pe in np.asarray(items, dtype=np.int64).reshape(-1, 8)[:, :4]:
+        used[seq, head, pb:pe] = True
+    if not used.any():
+        return 0, 0
+    return pool.format_mask_of(kt[used]) & pool.format_mask, vpool.format_mask_of(vt[used]) & vpool.format_mask
 
 
 def workspace_bytes(plan: DecodePlan, n_q: int, head_dim: int) -> int:
@@ -438,24 +591,40 @@ def decode_paged(
     need = workspace_bytes(plan, Q, hd)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=queries.device)
-    kp, vp = pool.c_pool(), vpool.c_pool()
-    if records is not None and records.k_mask > 0 and records.v_mask > 0:
-        # (checked fresh below: the masks are those of these tables' pages)
-        kp.format_mask, vp.format_mask = records.k_mask, records.v_mask
-    args = (kp, vp, C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
-            C.c_void_p(plan.items.data_ptr()), plan.n_items,
-            C.c_void_p(plan.merges.data_ptr() if plan.merges is not None and merge else 0),
-            plan.n_merges if merge else 0, C.c_void_p(queries.data_ptr()), dtype_code(queries), float(query_scale),
-            B, H, Q, C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()), int(workspace.numel()))
-    if records is None:
-        st = _lib.lib().dc_decode_paged(*args, C.c_void_p(current_stream_ptr()))
-    else:
-        if not records.fresh_for(plan, k_table, v_table, pool, vpool):
-            raise ValueError("page records are stale: gather them again after a change to the plan, the page "
-                             "tables or the pools' descriptors")
-        st = _lib.lib().dc_decode_paged_records(*args, C.c_void_p(records.data.data_ptr()), records.stride,
-                                                C.c_void_p(current_stream_ptr()))
-    _lib.check(st, "dc_decode_paged")
+    if records is not None and not records.fresh_for(plan, k_table, v_table, pool, vpool):
+        raise ValueError("page records are stale: gather them again after a change to the plan, the page "
+                         "tables or the pools' descriptors")
+    stream = C.c_void_p(current_stream_ptr())
+
+    def launch(first: int, count: int, with_merges: bool, masks) -> None:
+        """Items [first, first + count) in one launch (and the plan's merges
+        after it when ``with_merges``); ``masks``: the formats those items
+        read, from the page records, or None for the pools' masks."""
+        if count == 0:  # (a region plan whose pages are all in front)
+            if with_merges and merge:
+                merge_partials(plan, out, workspace)
+            return
+        kp, vp = pool.c_pool(), vpool.c_pool()
+        if masks is not None and masks[0] > 0 and masks[1] > 0:
+            # (records checked fresh above: the masks are those of these tables' pages)
+            kp.format_mask, vp.format_mask = masks
+        m_on = with_merges and merge and plan.merges is not None
+        args = (kp, vp, C.c_void_p(k_table.data_ptr()), C.c_void_p(v_table.data_ptr()), stride,
+                C.c_void_p(plan.items.data_ptr() + 32 * first), count,
+                C.c_void_p(plan.merges.data_ptr() if m_on else 0), plan.n_merges if m_on else 0,
+                C.c_void_p(queries.data_ptr()), dtype_code(queries), float(query_scale),
+                B, H, Q, C.c_void_p(out.data_ptr()), C.c_void_p(workspace.data_ptr()), int(workspace.numel()))
+        if records is None:
+            st = _lib.lib().dc_decode_paged(*args, stream)
+        else:
+            st = _lib.lib().dc_decode_paged_records(
+                *args, C.c_void_p(records.data.data_ptr() + 16 * records.stride * first), records.stride, stream)
+        _lib.check(st, "dc_decode_paged")
+
+    nf = int(plan.n_front)
+    if nf:  # region plan: the front items first, with their own formats
+        launch(0, nf, False, None if records is None else (records.front_k_mask, records.front_v_mask))
+    launch(nf, plan.n_items - nf, True, None if records is None else (records.k_mask, records.v_mask))
     return out
 
 

@@ -221,6 +221,10 @@ class DevicePagePool:
     def tokens_of(self, page_ids) -> np.ndarray:
         return self._host_desc["tokens"][np.asarray(page_ids, dtype=np.int64)].astype(np.int64)
 
+    def formats_of(self, page_ids) -> np.ndarray:
+        """The ``_lib.FMT_*`` format of each page id (same shape)."""
+        return self._host_desc["format"][np.asarray(page_ids, dtype=np.int64)].astype(np.int64)
+
     def format_mask_of(self, page_ids) -> int:
         """``dc_pool.format_mask`` bits of the formats these pages hold (a
         subset of :attr:`format_mask`)."""

@@ -16,7 +16,7 @@ import numpy as np
 from . import _lib
 from .config import PageModeSpec, choose_page_mode, make_explicit_policy
 from .decode import (DecodePlan, chunks_per_page, decode_paged, gather_records, launch_target_items, make_plan,
-                     merge_partials, page_costs, workspace_bytes)
+                     make_region_plan, merge_partials, page_costs, workspace_bytes)
 from .page_pool import DevicePagePool, PoolGeometry
 
 
@@ -259,14 +259,17 @@ def _gen(shape, gen, dist: str, device):
 def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | None = None, batch: int | None = None,
                    context: int | None = None, pages_per_split: int | None = None,
                    scatter_pages: bool = True, key_bits: int | None = None,
-                   replicas: int | None = None) -> Workload:
+                   replicas: int | None = None, window_launch: bool = True) -> Workload:
     """Encode every layer's pages on the device and build its page tables.
     ``layers`` / ``batch`` / ``context`` shrink the workload for tests (one
     KV set unless ``replicas`` says otherwise); ``replicas`` sets the number
     of independent KV sets the steps cycle through;
     ``scatter_pages=False`` keeps each sequence's pages in allocation order;
     ``key_bits`` re-codes the configuration's M0 key pages at that width
-    (a variant named ``<workload>_k<bits>``)."""
+    (a variant named ``<workload>_k<bits>``); ``window_launch`` (fill
+    plans of a workload with an exact recent window): the window's pages
+    run in a launch of their own ahead of the rest (``make_region_plan``),
+    so the bulk launch runs the kernel instance for its 4-bit pages only."""
     torch = _torch()
     spec = SPECS[name]
     if key_bits is not None and key_bits != spec.key.bits:
@@ -407,8 +410,24 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
         if pages_per_split is None:
             cost = page_costs(k_pool, v_pool, kids_tables[l], vids_tables[l], lt.seq_pages)
         last = k_pool.tokens_of(kids_tables[l][np.arange(B), 0, np.asarray(lt.seq_pages) - 1]).astype(np.int32)
-        wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp, page_cost=cost,
-                                  target_items=launch_target_items(k_pool, v_pool, Q), last_page_tokens=last))
+        front = _exact_window(k_pool, v_pool, kids_tables[l], vids_tables[l], lt.seq_pages) \
+            if (window_launch and spec.recent_window and pages_per_split is None) else None
+        if front is not None:
+            # the bulk launch: every page outside the window, at the waves
+            # per SIMD of its own formats
+            pg = np.arange(kids_tables[l].shape[2])[None, None, :]
+            outside = np.broadcast_to((pg < np.asarray(lt.seq_pages)[:, None, None])
+                                      & ~((pg >= front[:, 0, None, None]) & (pg < front[:, 1, None, None])),
+                                      kids_tables[l].shape)
+            km = k_pool.format_mask_of(kids_tables[l][outside])
+            vm = v_pool.format_mask_of(vids_tables[l][outside])
+            wl.plans.append(make_region_plan(lt.seq_pages, H, front, device=dev, chunks_per_page=cpp, page_cost=cost,
+                                             target_items=launch_target_items(k_pool, v_pool, Q, km, vm),
+                                             last_page_tokens=last))
+        else:
+            wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp,
+                                      page_cost=cost, target_items=launch_target_items(k_pool, v_pool, Q),
+                                      last_page_tokens=last))
     wl.plan = wl.plans[0]
     need = max(workspace_bytes(p, Q, hd) for p in wl.plans)
     wl.workspace = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)
@@ -426,6 +445,24 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
                   for l, lt in enumerate(tables)]
     torch.cuda.synchronize(dev)
     return wl
+
+
+def _exact_window(k_pool, v_pool, kt: np.ndarray, vt: np.ndarray, seq_pages) -> np.ndarray | None:
+    """Per sequence, the page range ``[begin, end)`` of its exact recent
+    window: the fp16 (M3) key and value pages, the same for every KV head
+    and contiguous.  None when some sequence has none or they do not form
+    one such range."""
+    out = np.zeros((kt.shape[0], 2), dtype=np.int64)
+    for b in range(kt.shape[0]):
+        n = int(seq_pages[b])
+        exact = (k_pool.formats_of(kt[b, :, :n]) == _lib.FMT_M3_F16) & (v_pool.formats_of(vt[b, :, :n]) == _lib.FMT_M3_F16)
+        if not np.all(exact == exact[0]) or not exact[0].any():
+            return None
+        idx = np.flatnonzero(exact[0])
+        if idx[-1] - idx[0] + 1 != idx.size:
+            return None
+        out[b] = (idx[0], idx[-1] + 1)
+    return out
 
 
 def _apply_recent_window(spec, k_pool, v_pool, kt, vt, n_pages, lengths, gen, dev, lt, layer):

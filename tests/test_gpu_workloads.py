@@ -182,3 +182,51 @@ def test_kv_sets_cycle_step_by_step():
         torch.cuda.synchronize()
         for l in wl.replica_layers(r):
             assert torch.equal(wl.outs[l], want[l]), f"set {r} layer {l} differs from the eager step"
+
+
+def test_c5_window_launch_matches_oracle_and_one_launch():
+    """Config 5's fill plans run each stream's exact fp16 window in a launch
+    of its own ahead of the 4-bit pages (a region plan, each launch on the
+    kernel instance of its own formats): every stream of two layers
+    against the oracle, and against the same pages planned as one launch;
+    then the captured step graph against the eager step, bit for bit."""
+    import torch
+
+    from dotcache_amd.decode import waves_per_simd
+    from dotcache_amd.workloads import build_workload
+
+    kw = dict(seed=5, layers=2, batch=3, context=3000)
+    wl = build_workload("c5", **kw)
+    plan = wl.plans[0]
+    assert plan.n_front > 0, "the window gets its own launch"
+    rec = wl.records[0]
+    assert waves_per_simd(wl.k_pool, wl.v_pool, wl.spec.gqa, rec.k_mask, rec.v_mask) == 2
+    print(f"c5 window launch: {plan.n_front} front items of {plan.n_items}", flush=True)
+    for _ in range(2):
+        wl.step()
+    torch.cuda.synchronize()
+    B, H = wl.spec.batch, wl.spec.n_kv_heads
+    for layer in range(2):
+        _check(wl, layer, [(b, h) for b in range(B) for h in range(H)])
+    one = build_workload("c5", window_launch=False, **kw)
+    assert one.plans[0].n_front == 0
+    for _ in range(2):
+        one.step()
+    torch.cuda.synchronize()
+    for layer in range(2):
+        err = float((wl.outs[layer] - one.outs[layer]).abs().max())
+        assert err < 2e-5, f"layer {layer}: window launch vs one launch differ by {err}"
+    want = [o.clone() for o in wl.outs]
+    wl.capture()
+    for rep in range(3):
+        for o in wl.outs:
+            o.fill_(float("nan"))
+        wl.step()
+        torch.cuda.synchronize()
+        for l, (o, w) in enumerate(zip(wl.outs, want)):
+            # (each step appends the same token again into slot 0 of the tail)
+            assert torch.equal(o, w), f"replay {rep} layer {l} differs from the eager step"
+        graph, wl.graph = wl.graph, None
+        wl.step()
+        torch.cuda.synchronize()
+        wl.graph = graph
