@@ -53,9 +53,11 @@ def parse():
                          "configuration's own line)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from Python each step instead of replaying captured HIP graphs")
-    ap.add_argument("--one-launch", action="store_true",
-                    help="run an exact recent window (c5) in the same decode launch as the 4-bit pages instead of "
-                         "a launch of its own")
+    ap.add_argument("--window", default="merge", choices=["merge", "launch", "none"],
+                    help="where an exact recent window (c5) is attended: in the split-K merge (default), in a "
+                         "decode launch of its own, or in the same decode launch as the 4-bit pages")
+    ap.add_argument("--front-items", type=int, default=None,
+                    help="items of the exact window's launch (default: one per 32-token chunk)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--shortlist-pages", type=int, default=0, metavar="N",
                     help="only time the execution shortlist kernels: relevance of N pages (4-row sketches, "
@@ -377,7 +379,7 @@ def main():
     set_mfma_head_block(args.head_block)
     wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
                         scatter_pages=not args.contiguous_pages, key_bits=args.key_bits,
-                        window_launch=not args.one_launch)
+                        window=args.window, front_items=args.front_items)
     spec = wl.spec
     # "fill": per-layer plans of a launch's item budget cut at 32-token chunks
     # by page cost; "pages": --pages-per-split whole-page splits
@@ -487,7 +489,9 @@ def main():
     value = pos_step / (ms_step / 1e3)
     ms_step_median = float(np.median(step_ms))
     gbps = bytes_step / (ms_step / 1e3) / 1e9
-    bytes_launch = bytes_step / L
+    # (the decode launches read every page but those the merges attend)
+    win_bytes = wl.window_bytes_per_step()
+    bytes_launch = (bytes_step - win_bytes) / L
     achieved = bytes_launch / (launch_ms / 1e3) / 1e9
     log(f"{ms_step:.3f} ms/step (median {ms_step_median:.3f} over {n_med}), {value / 1e9:.3f} G tokens/s, "
         f"{gbps:.0f} GB/s over the step; "
@@ -536,6 +540,7 @@ def main():
             "page_records": bool(wl.records),
             "pages_per_split": wl.plan.pages_per_split,
             "decode_launches_per_layer": 2 if wl.plan.n_front else 1,
+            "window": args.window if spec.recent_window else None,
             "launch": "eager" if args.eager else "hip graph of the whole step",
             "parallelism": "single GPU",
         },
@@ -553,13 +558,15 @@ def main():
                                         args.head_block),
             "kernel": ("decode_generic_kernel" if args.decode_path == "generic" else "decode_mfma_kernel")
                       + (" (dc_decode_paged: the exact window's launch, then the rest's; launch_us is both)"
-                         if wl.plan.n_front else " (dc_decode_paged, one launch per layer)"),
+                         if wl.plan.n_front else " (dc_decode_paged, one launch per layer"
+                         + ("; the exact window is read by the merge)" if wl.plan.host_windows is not None else ")")),
             "launch_us": launch_ms * 1e3,
             "launch_us_stat": f"mean over {n_med} replays of one step's {L} decode launches (event per replay)",
             "launch_us_median": float(np.median(dec_ms)) * 1e3,
             "launch_us_p10_p90": [float(np.percentile(dec_ms, 10)) * 1e3, float(np.percentile(dec_ms, 90)) * 1e3],
             "frac_at_median_launch": bytes_launch / (float(np.median(dec_ms)) / 1e3) / 1e9 / HBM_PEAK_GBPS,
             "bytes_per_launch": bytes_launch,
+            "merge_window_bytes_per_layer": win_bytes / L,
             "merge_us": merge_ms * 1e3,
             "decode_path": args.decode_path,
             "head_block": args.head_block,

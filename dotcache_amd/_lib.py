@@ -104,6 +104,9 @@ SIGNATURES = {
     "dc_set_mfma_head_block": (C.c_int, [C.c_int32]),
     "dc_lse_merge": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                C.c_void_p, C.c_void_p]),
+    "dc_window_merge": (C.c_int, [Pool, Pool, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_int32,
+                                  C.c_void_p, C.c_int32, C.c_float, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                                  C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
 }
 
 _lib: C.CDLL | None = None

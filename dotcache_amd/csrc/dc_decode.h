@@ -59,6 +59,12 @@ int launch_decode_generic(const DecodeArgs& a, hipStream_t stream);
 // Launches the MFMA kernel when every format in the pools' masks and the
 // geometry fit it; *launched tells the caller whether to fall back.
 int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched);
-int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream);
+int launch_merge(const DecodeArgs& a, const dc_merge_item* merges, int32_t n_merges, hipStream_t stream,
+                 const dc_window_range* windows = nullptr);
+
+// Windows a merge attends (dc_window_merge): at most this many tokens in at
+// most this many pages.
+constexpr int kMaxWinTokens = 256;
+constexpr int kMaxWinPages = 8;
 
 }  // namespace dc

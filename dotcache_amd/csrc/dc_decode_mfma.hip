@@ -1541,6 +1541,7 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   DC_EXACT(128, 32, KEYS_M0, 4, 4, false, true, true, 4)
   DC_EXACT(256, 32, KEYS_MIXED, 4, 4, true, true, true, 4)  // config 5 (fp16 recent window)
   DC_EXACT(256, 32, KEYS_M0, 4, 4, false, true, true, 4)
+  DC_EXACT(256, 32, KEYS_M3, 4, 4, true, false, false, 4)  // config 5's window launch (fp16 keys and values)
   DC_EXACT(128, 32, KEYS_M0, 8, 4, false, true, true, 4)  // 8-bit keys, 4-bit values
   DC_EXACT(128, 32, KEYS_M0, 8, 8, false, true, true, 4)  // 8-bit keys and values
   DC_GENERAL(64, 32, 4)

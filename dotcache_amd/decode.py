@@ -66,6 +66,11 @@ class DecodePlan:
     # (make_region_plan: the pages of a different format mix, such as an
     # exact recent window, kept out of the bulk launch's kernel instance)
     n_front: int = 0
+    # region plans with window_merge: per merge item the page range
+    # [begin, end) of its stream that the merge itself attends
+    # (dc_window_merge; fp16 key and value pages), device int32 [n_merges, 2]
+    windows: object | None = None
+    host_windows: np.ndarray | None = None
 
     def check(self, seq_pages: np.ndarray, n_kv_heads: int, table_stride: int, chunks_per_page: int = 1) -> None:
         """Raise ValueError unless every work item and merge item of the plan
@@ -317,7 +322,7 @@ def _fill_units(unit_pages: np.ndarray, unit_last: np.ndarray, unit_cost, cpp: i
 
 def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks_per_page: int = 1, page_cost=None,
                      last_page_tokens=None, target_items: int | None = None, front_items: int | None = None,
-                     front_min_chunks: int = 1) -> DecodePlan:
+                     front_min_chunks: int = 1, window_merge: bool = False) -> DecodePlan:
     """A fill plan in two launches: pages ``[front[b, 0], front[b, 1])`` of
     every stream of sequence b (``front``: int ``[n_seqs, 2]``, an empty
     range for none) are cut into ``front_items`` items (default: one per
@@ -329,7 +334,12 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
     pages of another format (an exact fp16 recent window among 4-bit
     pages) do not hold the bulk launch to the instance that reads both
     (``decode_paged``, with page records).  Arguments otherwise as for
-    :func:`make_plan` (fill plans only)."""
+    :func:`make_plan` (fill plans only).
+
+    ``window_merge``: no front launch; the merge of every stream attends its
+    front pages itself (``dc_window_merge``: fp16 key and value pages, at
+    most 256 tokens in 8 pages per stream), so the plan has one merge item
+    per stream and one launch."""
     torch = _torch()
     sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
     if sp.ndim != 1 or sp.size == 0 or np.any(sp <= 0):
@@ -347,8 +357,15 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
     if cost is not None and (cost.ndim != 3 or cost.shape[:2] != (B, H) or cost.shape[2] < int(sp.max())):
         raise ValueError("page_cost must have shape [n_seqs, n_kv_heads, >= max pages]")
     target = int(target_items) if target_items else default_target_items()
+    if window_merge:
+        wtok = [sum(full if p + 1 < sp[b] else int(last[b]) for p in range(int(fr[b, 0]), int(fr[b, 1])))
+                for b in range(B)]
+        if np.any(fr[:, 1] - fr[:, 0] > 8) or max(wtok) > 256:
+            raise ValueError("window_merge: a window holds at most 256 tokens in at most 8 pages")
+        if np.any((fr[:, 0] == 0) & (fr[:, 1] == sp)):
+            raise ValueError("window_merge: every stream needs pages outside its window")
     key = ("region", sp.tobytes(), H, fr.tobytes(), cpp, None if cost is None else cost.tobytes(), last.tobytes(),
-           target, front_items, int(front_min_chunks), str(device))
+           target, front_items, int(front_min_chunks), bool(window_merge), str(device))
     hit = _plan_cache.get(key)
     if hit is not None:
         return hit
@@ -376,6 +393,8 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
     front_units = [(b, h, int(fr[b, 0]), int(fr[b, 1])) for b in range(B) for h in range(H) if fr[b, 1] > fr[b, 0]]
     bulk_units = [(b, h, p0, p1) for b in range(B) for h in range(H)
                   for p0, p1 in ((0, int(fr[b, 0])), (int(fr[b, 1]), int(sp[b]))) if p1 > p0]
+    if window_merge:
+        front_units = []
     if front_items is None:  # one item per chunk that holds tokens
         front_items = sum((p1 - p0 - 1) * cpp + (min(cpp, (int(last[b]) + 31) // 32) if p1 == sp[b] else cpp)
                           for b, h, p0, p1 in front_units)
@@ -384,11 +403,12 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
     items = np.concatenate([f_it, b_it]) if len(f_it) else b_it
     # partial slots: every stream's items (front and bulk) take consecutive
     # slots, merged by one merge item; a stream of one item writes its output
+    # (with window_merge every stream has a merge item: it attends the window)
     stream = items[:, 0].astype(np.int64) * H + items[:, 1]
     merges, n_part = [], 0
     for s in np.unique(stream):
         rows = np.flatnonzero(stream == s)
-        if len(rows) == 1:
+        if len(rows) == 1 and not window_merge:
             items[rows[0], 4] = -1
             continue
         items[rows, 4] = n_part + np.arange(len(rows), dtype=np.int32)
@@ -401,6 +421,10 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
     big = max(f_big, b_big)
     plan = DecodePlan(dev_items, dev_merges, len(items), len(merges), n_part, -(-big // cpp), items, host_merges,
                       chunks_per_page=cpp, largest_chunks=big, n_front=len(f_it))
+    if window_merge:
+        hw = np.ascontiguousarray(fr[host_merges[:, 0]], dtype=np.int32).reshape(-1, 2)
+        plan.host_windows = hw
+        plan.windows = torch.from_numpy(hw.ravel().view(np.uint8).copy()).to(device) if len(hw) else None
     if len(_plan_cache) > 256:
         _plan_cache.clear()
     _plan_cache[key] = plan
@@ -455,6 +479,9 @@ class PageRecords:
     # pages, these the front items'
     front_k_mask: int = -1
     front_v_mask: int = -1
+    # plans with merge windows: [n_merges][8] (key, value) descriptor pairs
+    # of each window's pages, for dc_window_merge
+    windows: object = None
 
     @staticmethod
     def versions_of(k_table, v_table, pool, vpool) -> tuple:
@@ -489,7 +516,17 @@ def gather_records(pool: DevicePagePool, k_table, v_table, seq_pages, plan: Deco
     # the formats of every page the plan reads (pages [0, seq_pages[b]) of
     # every row; per launch for region plans)
     kt, vt = k_table.cpu().numpy(), v_table.cpu().numpy()
-    if plan.n_front:
+    win = None
+    if plan.host_windows is not None:
+        check_windows(pool, vpool, kt, vt, plan)
+        k_mask, v_mask = items_format_masks(pool, vpool, kt, vt, it)
+        fk = fv = -1
+        wr = np.zeros((plan.n_merges, 8, 2), dtype=pool.descs_of([0]).dtype)
+        for m, ((seq, head, _, _), (pb, pe)) in enumerate(zip(plan.host_merges, plan.host_windows)):
+            wr[m, : pe - pb, 0] = pool.descs_of(kt[seq, head, pb:pe])
+            wr[m, : pe - pb, 1] = vpool.descs_of(vt[seq, head, pb:pe])
+        win = torch.from_numpy(wr.view(np.uint8).ravel().copy()).to(k_table.device)
+    elif plan.n_front:
         (fk, fv), (k_mask, v_mask) = (items_format_masks(pool, vpool, kt, vt, part)
                                       for part in (it[: plan.n_front], it[plan.n_front:]))
     else:
@@ -498,7 +535,23 @@ def gather_records(pool: DevicePagePool, k_table, v_table, seq_pages, plan: Deco
         v_mask = vpool.format_mask_of(vt[live]) & vpool.format_mask
         fk = fv = -1
     return PageRecords(data, rs, plan, (k_table, v_table, pool, vpool),
-                       PageRecords.versions_of(k_table, v_table, pool, vpool), k_mask, v_mask, fk, fv)
+                       PageRecords.versions_of(k_table, v_table, pool, vpool), k_mask, v_mask, fk, fv, win)
+
+
+def check_windows(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray, plan: DecodePlan) -> None:
+    """Raise ValueError unless every window of ``plan`` (``window_merge``)
+    holds only fp16 (M3 f16) key and value pages of equal token counts, the
+    only pages ``dc_window_merge`` reads (it skips others)."""
+    for (seq, head, _, _), (pb, pe) in zip(np.asarray(plan.host_merges).reshape(-1, 4),
+                                           np.asarray(plan.host_windows).reshape(-1, 2)):
+        if pe <= pb:
+            continue
+        kid, vid = kt[seq, head, pb:pe], vt[seq, head, pb:pe]
+        pool.validate_ids(kid)
+        vpool.validate_ids(vid)
+        if (np.any(pool.formats_of(kid) != _lib.FMT_M3_F16) or np.any(vpool.formats_of(vid) != _lib.FMT_M3_F16)
+                or not np.array_equal(pool.tokens_of(kid), vpool.tokens_of(vid))):
+            raise ValueError("a merge window holds a page that is not an fp16 (M3) key / value page pair")
 
 
 def items_format_masks(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray,
@@ -545,7 +598,9 @@ def decode_paged(
     partials in ``workspace`` for :func:`merge_partials` (sequences that
     were not split are written to ``out`` either way).  ``records``: page
     records of ``plan`` (:func:`gather_records`) over these tables and
-    pools; stale records raise ValueError.
+    pools; stale records raise ValueError.  A region plan
+    (``make_region_plan``) runs as two launches: its front items, then the
+    rest and the merges.
     """
     torch = _torch()
     vpool = pool if v_pool is None else v_pool
@@ -624,19 +679,54 @@ def decode_paged(
     nf = int(plan.n_front)
     if nf:  # region plan: the front items first, with their own formats
         launch(0, nf, False, None if records is None else (records.front_k_mask, records.front_v_mask))
-    launch(nf, plan.n_items - nf, True, None if records is None else (records.k_mask, records.v_mask))
+    windowed = plan.host_windows is not None
+    if windowed and validate:
+        check_windows(pool, vpool, kt, vt, plan)
+    launch(nf, plan.n_items - nf, not windowed, None if records is None else (records.k_mask, records.v_mask))
+    if windowed and merge:
+        merge_partials(plan, out, workspace, window=(pool, vpool, k_table, v_table, queries, query_scale),
+                       records=records)
     return out
 
 
-def merge_partials(plan: DecodePlan, out, workspace) -> None:
+def merge_partials(plan: DecodePlan, out, workspace, *, window=None, records: PageRecords | None = None) -> None:
     """The split-K log-sum-exp merge of ``plan`` on its own
-    (``dc_lse_merge``): partials in ``workspace`` -> ``out``."""
+    (``dc_lse_merge``): partials in ``workspace`` -> ``out``.  A plan with
+    merge windows (``make_region_plan(window_merge=True)``) needs
+    ``window = (pool, v_pool, k_table, v_table, queries, query_scale)`` of
+    its decode: the merge attends those pages too (``dc_window_merge``),
+    reading their descriptors from ``records`` (``gather_records`` of the
+    plan over those tables) when given."""
     if plan.n_merges == 0:
         return
     B, H, Q, hd = (int(x) for x in out.shape)
     m = np.asarray(plan.host_merges, dtype=np.int64).reshape(-1, 4)
     if np.any((m[:, 0] < 0) | (m[:, 0] >= B)) or np.any((m[:, 1] < 0) | (m[:, 1] >= H)):
         raise ValueError("plan: a merge item names a sequence or KV head outside the output")
+    if plan.host_windows is not None:
+        if window is None:
+            raise ValueError("this plan's merges attend window pages: pass window=(pool, v_pool, k_table, v_table, "
+                             "queries, query_scale)")
+        pool, vpool, k_table, v_table, queries, query_scale = window
+        vpool = pool if vpool is None else vpool
+        if tuple(queries.shape) != (B, H, Q, hd) or not queries.is_contiguous():
+            raise ValueError("window merge: queries must be contiguous [n_seqs, n_kv_heads, n_q, head_dim]")
+        win = None
+        if records is not None:
+            if not records.fresh_for(plan, k_table, v_table, pool, vpool):
+                raise ValueError("page records are stale: gather them again after a change to the plan, the page "
+                                 "tables or the pools' descriptors")
+            win = records.windows
+        st = _lib.lib().dc_window_merge(pool.c_pool(), vpool.c_pool(), C.c_void_p(k_table.data_ptr()),
+                                        C.c_void_p(v_table.data_ptr()), int(k_table.shape[2]),
+                                        C.c_void_p(plan.merges.data_ptr()), C.c_void_p(plan.windows.data_ptr()),
+                                        plan.n_merges, C.c_void_p(queries.data_ptr()), dtype_code(queries),
+                                        float(query_scale), B, H, Q, C.c_void_p(out.data_ptr()),
+                                        C.c_void_p(workspace.data_ptr()), int(workspace.numel()),
+                                        C.c_void_p(win.data_ptr() if win is not None else 0),
+                                        C.c_void_p(current_stream_ptr()))
+        _lib.check(st, "dc_window_merge")
+        return
     st = _lib.lib().dc_lse_merge(C.c_void_p(plan.merges.data_ptr()), plan.n_merges, C.c_void_p(workspace.data_ptr()),
                                  int(workspace.numel()), B, H, Q, hd, C.c_void_p(out.data_ptr()),
                                  C.c_void_p(current_stream_ptr()))

@@ -221,6 +221,10 @@ class DevicePagePool:
     def tokens_of(self, page_ids) -> np.ndarray:
         return self._host_desc["tokens"][np.asarray(page_ids, dtype=np.int64)].astype(np.int64)
 
+    def descs_of(self, page_ids) -> np.ndarray:
+        """Host copies of these pages' ``dc_page_desc`` records (``DESC_DTYPE``)."""
+        return self._host_desc[np.asarray(page_ids, dtype=np.int64)].copy()
+
     def formats_of(self, page_ids) -> np.ndarray:
         """The ``_lib.FMT_*`` format of each page id (same shape)."""
         return self._host_desc["format"][np.asarray(page_ids, dtype=np.int64)].astype(np.int64)

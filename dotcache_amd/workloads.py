@@ -164,6 +164,22 @@ class Workload:
             total += 8 * len(self.k_page_ids_by_layer[l])
         return total
 
+    def window_bytes_per_step(self) -> int:
+        """Of :meth:`algorithmic_bytes_per_step`, the bytes of the pages the
+        merges attend (plans with merge windows), which no decode launch
+        reads: their fp16 keys and values and table entries."""
+        total = 0
+        for l in self.replica_layers(0):
+            plan = self.plans[l]
+            if plan.host_windows is None:
+                continue
+            kt = self.layers[l].k_table.cpu().numpy()
+            vt = self.layers[l].v_table.cpu().numpy()
+            for (seq, head, _, _), (pb, pe) in zip(plan.host_merges, plan.host_windows):
+                total += self.k_pool.read_bytes(kt[seq, head, pb:pe]) + self.v_pool.read_bytes(vt[seq, head, pb:pe])
+                total += 8 * int(pe - pb)
+        return total
+
     def token_positions_per_step(self) -> int:
         """(sequence, layer, context token) positions attended per step."""
         return int(np.sum(self.attended_lengths())) * self.spec.n_layers
@@ -197,7 +213,10 @@ class Workload:
         self.decode_kernel(l)
 
     def merge_kernel(self, l: int) -> None:
-        merge_partials(self.plans[l], self.outs[l], self.workspace)
+        lt = self.layers[l]
+        merge_partials(self.plans[l], self.outs[l], self.workspace,
+                       window=(self.k_pool, self.v_pool, lt.k_table, lt.v_table, self.queries[l], self.query_scale),
+                       records=self.records[l] if self.records else None)
 
     def decode_kernel(self, l: int) -> None:
         """Layer ``l``'s decode kernel alone (``dc_decode_paged_records``
@@ -259,17 +278,23 @@ def _gen(shape, gen, dist: str, device):
 def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | None = None, batch: int | None = None,
                    context: int | None = None, pages_per_split: int | None = None,
                    scatter_pages: bool = True, key_bits: int | None = None,
-                   replicas: int | None = None, window_launch: bool = True) -> Workload:
+                   replicas: int | None = None, window: str = "merge",
+                   front_items: int | None = None) -> Workload:
     """Encode every layer's pages on the device and build its page tables.
     ``layers`` / ``batch`` / ``context`` shrink the workload for tests (one
     KV set unless ``replicas`` says otherwise); ``replicas`` sets the number
     of independent KV sets the steps cycle through;
     ``scatter_pages=False`` keeps each sequence's pages in allocation order;
     ``key_bits`` re-codes the configuration's M0 key pages at that width
-    (a variant named ``<workload>_k<bits>``); ``window_launch`` (fill
-    plans of a workload with an exact recent window): the window's pages
-    run in a launch of their own ahead of the rest (``make_region_plan``),
-    so the bulk launch runs the kernel instance for its 4-bit pages only."""
+    (a variant named ``<workload>_k<bits>``); ``window`` (fill plans of a
+    workload with an exact recent window): ``"merge"`` attends the window's
+    fp16 pages in the split-K merge (``make_region_plan(window_merge=True)``),
+    ``"launch"`` in a decode launch of its own ahead of the rest
+    (``front_items`` items, default one per chunk), either way keeping the
+    decode launch to the kernel instance of its 4-bit pages; ``"none"``
+    decodes them with the rest in one launch."""
+    if window not in ("merge", "launch", "none"):
+        raise ValueError("window must be 'merge', 'launch' or 'none'")
     torch = _torch()
     spec = SPECS[name]
     if key_bits is not None and key_bits != spec.key.bits:
@@ -411,7 +436,7 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
             cost = page_costs(k_pool, v_pool, kids_tables[l], vids_tables[l], lt.seq_pages)
         last = k_pool.tokens_of(kids_tables[l][np.arange(B), 0, np.asarray(lt.seq_pages) - 1]).astype(np.int32)
         front = _exact_window(k_pool, v_pool, kids_tables[l], vids_tables[l], lt.seq_pages) \
-            if (window_launch and spec.recent_window and pages_per_split is None) else None
+            if (window != "none" and spec.recent_window and pages_per_split is None) else None
         if front is not None:
             # the bulk launch: every page outside the window, at the waves
             # per SIMD of its own formats
@@ -423,7 +448,8 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
             vm = v_pool.format_mask_of(vids_tables[l][outside])
             wl.plans.append(make_region_plan(lt.seq_pages, H, front, device=dev, chunks_per_page=cpp, page_cost=cost,
                                              target_items=launch_target_items(k_pool, v_pool, Q, km, vm),
-                                             last_page_tokens=last))
+                                             last_page_tokens=last, front_items=front_items,
+                                             window_merge=window == "merge"))
         else:
             wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp,
                                       page_cost=cost, target_items=launch_target_items(k_pool, v_pool, Q),

@@ -131,6 +131,14 @@ typedef struct dc_merge_item {
   int32_t count;
 } dc_merge_item;
 
+/* Pages [page_begin, page_end) of a merge item's stream that the merge
+ * itself attends (dc_window_merge): fp16 (M3) key and value pages, such as
+ * an exact recent window, read by no work item. */
+typedef struct dc_window_range {
+  int32_t page_begin;
+  int32_t page_end;
+} dc_window_range;
+
 /* ---- library ---------------------------------------------------------- */
 
 /* Message for the last non-zero status returned on this thread. */
@@ -376,6 +384,27 @@ int64_t dc_decode_workspace_bytes(int32_t n_partials, int32_t n_q, int32_t head_
  * combine across chunks). */
 int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const void* workspace, int64_t workspace_bytes,
                  int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, int32_t head_dim, float* out, dc_stream_t stream);
+
+/* dc_lse_merge that also attends, for every merge item m, the fp16 (M3 f16)
+ * key and value pages windows[m] of its stream (through the tables, like
+ * the decode) before it combines: the window's (m, l, o) joins the
+ * item's partials in the log-sum-exp.  A stream's few exact pages (the
+ * recent window kept in fp16 among 4-bit pages) then need no decode
+ * launch of their own, and the decode launch keeps the kernel instance of
+ * the 4-bit pages.  A window holds at most 256 tokens in at most 8 pages;
+ * head_dim must be 64, 128 or 256; out and the workspace 16-byte aligned.
+ * Pages of another format in a window are skipped (hosts validate them).
+ * records: NULL, or device [n_merges][8] key / value descriptor pairs of
+ * each window's pages in order (a host snapshot of the tables and
+ * descriptors), read instead of the tables and descriptor arrays.
+ * Replaces, for those pages, the same score / softmax / mix as
+ * dc_decode_paged (reference dotcache/attention_runtime.py:260-315,
+ * dotcache/backends/torch_mps.py:4276-4435). */
+int dc_window_merge(dc_pool k_pool, dc_pool v_pool, const int32_t* k_table, const int32_t* v_table,
+                    int32_t table_stride, const dc_merge_item* merges, const dc_window_range* windows,
+                    int32_t n_merges, const void* queries, int32_t queries_dtype, float query_scale,
+                    int32_t n_seqs, int32_t n_kv_heads, int32_t n_q, float* out, const void* workspace,
+                    int64_t workspace_bytes, const dc_page_record* records, dc_stream_t stream);
 
 /* dc_decode_paged without a workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,

@@ -184,38 +184,44 @@ def test_kv_sets_cycle_step_by_step():
             assert torch.equal(wl.outs[l], want[l]), f"set {r} layer {l} differs from the eager step"
 
 
-def test_c5_window_launch_matches_oracle_and_one_launch():
-    """Config 5's fill plans run each stream's exact fp16 window in a launch
-    of its own ahead of the 4-bit pages (a region plan, each launch on the
-    kernel instance of its own formats): every stream of two layers
-    against the oracle, and against the same pages planned as one launch;
-    then the captured step graph against the eager step, bit for bit."""
+@pytest.mark.parametrize("window", ["merge", "launch"])
+def test_c5_window_matches_oracle_and_one_launch(window):
+    """Config 5's fill plans keep the exact fp16 window out of the decode
+    launch (a region plan): attended by the split-K merge ("merge") or by a
+    decode launch of its own ("launch"), so the decode launch runs the
+    kernel instance of the 4-bit pages.  Every stream of two layers against
+    the oracle, and against the same pages decoded in one launch; then the
+    captured step graph against the eager step, bit for bit."""
     import torch
 
     from dotcache_amd.decode import waves_per_simd
     from dotcache_amd.workloads import build_workload
 
     kw = dict(seed=5, layers=2, batch=3, context=3000)
-    wl = build_workload("c5", **kw)
+    wl = build_workload("c5", window=window, **kw)
     plan = wl.plans[0]
-    assert plan.n_front > 0, "the window gets its own launch"
+    if window == "merge":
+        assert plan.n_front == 0 and plan.host_windows is not None and plan.n_merges == 3 * wl.spec.n_kv_heads
+        assert np.all(plan.host_windows[:, 1] > plan.host_windows[:, 0])
+    else:
+        assert plan.n_front > 0, "the window gets its own launch"
     rec = wl.records[0]
     assert waves_per_simd(wl.k_pool, wl.v_pool, wl.spec.gqa, rec.k_mask, rec.v_mask) == 2
-    print(f"c5 window launch: {plan.n_front} front items of {plan.n_items}", flush=True)
+    print(f"c5 window {window}: {plan.n_front} front items of {plan.n_items}", flush=True)
     for _ in range(2):
         wl.step()
     torch.cuda.synchronize()
     B, H = wl.spec.batch, wl.spec.n_kv_heads
     for layer in range(2):
         _check(wl, layer, [(b, h) for b in range(B) for h in range(H)])
-    one = build_workload("c5", window_launch=False, **kw)
-    assert one.plans[0].n_front == 0
+    one = build_workload("c5", window="none", **kw)
+    assert one.plans[0].n_front == 0 and one.plans[0].host_windows is None
     for _ in range(2):
         one.step()
     torch.cuda.synchronize()
     for layer in range(2):
         err = float((wl.outs[layer] - one.outs[layer]).abs().max())
-        assert err < 2e-5, f"layer {layer}: window launch vs one launch differ by {err}"
+        assert err < 2e-5, f"layer {layer}: window {window} vs one launch differ by {err}"
     want = [o.clone() for o in wl.outs]
     wl.capture()
     for rep in range(3):
