@@ -73,7 +73,8 @@ def parse():
     return ap.parse_args()
 
 
-def profiled_traffic(workload: str, plan: str, pages_per_split: int, decode_path: str, head_block: int):
+def profiled_traffic(workload: str, plan: str, pages_per_split: int, decode_path: str, head_block: int,
+                     window: str | None = None):
     """HBM bytes per decode launch measured for this workload and plan by
     the FETCH_SIZE / WRITE_SIZE runs summarised under profiles/ (calibrated
     against a copy of known size there), or None if none matches."""
@@ -83,7 +84,8 @@ def profiled_traffic(workload: str, plan: str, pages_per_split: int, decode_path
         for m in re.finditer(r"<!-- traffic (\{.*?\}) -->", f.read_text()):
             rec = json.loads(m.group(1))
             if (rec.get("workload"), rec.get("plan"), rec.get("pages_per_split"), rec.get("decode_path"),
-                    rec.get("head_block")) == (workload, plan, pages_per_split, decode_path, head_block):
+                    rec.get("head_block"), rec.get("window")) == (workload, plan, pages_per_split, decode_path,
+                                                                 head_block, window):
                 return float(rec["traffic_bytes"])
     return None
 
@@ -555,7 +557,7 @@ def main():
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
             "traffic": profiled_traffic(spec.name, plan_kind, wl.plan.pages_per_split, args.decode_path,
-                                        args.head_block),
+                                        args.head_block, args.window if spec.recent_window else None),
             "kernel": ("decode_generic_kernel" if args.decode_path == "generic" else "decode_mfma_kernel")
                       + (" (dc_decode_paged: the exact window's launch, then the rest's; launch_us is both)"
                          if wl.plan.n_front else " (dc_decode_paged, one launch per layer"
