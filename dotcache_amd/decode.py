@@ -586,6 +586,7 @@ def decode_paged(
     v_pool: DevicePagePool | None = None,
     merge: bool = True,
     records: PageRecords | None = None,
+    page_masks: tuple[int, int] | None = None,
 ):
     """Fused decode for ``queries [n_seqs, n_kv_heads, n_q, head_dim]``.
 
@@ -600,7 +601,10 @@ def decode_paged(
     records of ``plan`` (:func:`gather_records`) over these tables and
     pools; stale records raise ValueError.  A region plan
     (``make_region_plan``) runs as two launches: its front items, then the
-    rest and the merges.
+    rest and the merges.  ``page_masks`` (without records, plans with no
+    front items): the ``format_mask`` bits of the key and value pages the
+    work items read, when narrower than the pools' (the launch then takes
+    the kernel instance of those formats; ``validate`` checks them).
     """
     torch = _torch()
     vpool = pool if v_pool is None else v_pool
@@ -682,7 +686,16 @@ def decode_paged(
     windowed = plan.host_windows is not None
     if windowed and validate:
         check_windows(pool, vpool, kt, vt, plan)
-    launch(nf, plan.n_items - nf, not windowed, None if records is None else (records.k_mask, records.v_mask))
+    masks = None if records is None else (records.k_mask, records.v_mask)
+    if masks is None and page_masks is not None:
+        if nf:
+            raise ValueError("page_masks apply to plans without front items")
+        masks = (int(page_masks[0]) & pool.format_mask, int(page_masks[1]) & vpool.format_mask)
+        if validate:
+            have = items_format_masks(pool, vpool, kt, vt, np.asarray(plan.host_items)[nf:])
+            if (have[0] & ~masks[0]) or (have[1] & ~masks[1]):
+                raise ValueError("page_masks leave out formats of pages the plan reads")
+    launch(nf, plan.n_items - nf, not windowed, masks)
     if windowed and merge:
         merge_partials(plan, out, workspace, window=(pool, vpool, k_table, v_table, queries, query_scale),
                        records=records)

@@ -119,6 +119,15 @@ def test_prefill_append_decode_matches_oracle(page_tokens, case):
         t += n
     ctx = _finalise_contexts(P, T0, steps, T1)
     _check_decode(cache, keys, values, T0, cfg, rng, page_context=ctx)
+    # the fp16 tail (5 tokens) was attended by the split-K merge, and the
+    # decode launch read only the other pages (with 16-token pages under the
+    # recent window every page is exact: one launch reads them all)
+    k_table, _, seq_pages, _ = cache._layer_tables(0)
+    front = cache._merge_windows(*cache._host_tables[0], seq_pages)
+    if case == "mode_override" or P == 64:
+        assert front is not None and np.all(front[:, 1] == seq_pages) and np.all(front[:, 0] >= 1)
+    else:
+        assert front is None
     for t, n in steps:
         for layer in range(L):
             cache.append_step(layer, keys[layer, :, :, t:t + n], torch.from_numpy(values[layer, :, :, t:t + n]), t)
