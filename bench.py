@@ -58,6 +58,9 @@ def parse():
                          "decode launch of its own, or in the same decode launch as the 4-bit pages")
     ap.add_argument("--front-items", type=int, default=None,
                     help="items of the exact window's launch (default: one per 32-token chunk)")
+    ap.add_argument("--lead-ratio", type=float, default=None,
+                    help="lead-trail plans for two-waves-per-SIMD instances with this lead/trail ratio "
+                         "(default: the library's; 0: plain plans)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--shortlist-pages", type=int, default=0, metavar="N",
                     help="only time the execution shortlist kernels: relevance of N pages (4-row sketches, "
@@ -381,7 +384,8 @@ def main():
     set_mfma_head_block(args.head_block)
     wl = build_workload(args.config, seed=args.seed, pages_per_split=args.pages_per_split,
                         scatter_pages=not args.contiguous_pages, key_bits=args.key_bits,
-                        window=args.window, front_items=args.front_items)
+                        window=args.window, front_items=args.front_items,
+                        lead_ratio="auto" if args.lead_ratio is None else (args.lead_ratio or None))
     spec = wl.spec
     # "fill": per-layer plans of a launch's item budget cut at 32-token chunks
     # by page cost; "pages": --pages-per-split whole-page splits
@@ -542,6 +546,7 @@ def main():
             "page_records": bool(wl.records),
             "pages_per_split": wl.plan.pages_per_split,
             "decode_launches_per_layer": 2 if wl.plan.n_front else 1,
+            "lead_ratio": max((r for r in wl.lead_ratios if r), default=None),
             "window": args.window if spec.recent_window else None,
             "launch": "eager" if args.eager else "hip graph of the whole step",
             "parallelism": "single GPU",

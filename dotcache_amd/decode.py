@@ -41,6 +41,14 @@ MIN_CHUNKS_PER_SPLIT = 2
 # took a wave 2.4 us and one of fp16 keys and values (32 KiB) 5.4 us: about
 # 1.0 us plus 7.5 GB/s per wave, and 1.0 us is worth about 8 KiB at that rate.
 CHUNK_COST_BYTES = 8192
+# Instances built for two waves per SIMD: the first wave placed on a SIMD
+# (blocks [0, n_simd) of a launch; block b + n_simd joins block b's SIMD)
+# issues first whenever both are ready, so with equal items it finished
+# first (C5: 91 against 123 us; C4: 26 against 33 us) and the second one
+# then ran alone.  Lead-trail plans (``lead_ratio``) cut each SIMD's share
+# into a lead item, placed in the first half of the launch, and a trail
+# item this many times smaller in the second.
+LEAD_RATIO = 1.6
 
 
 def _torch():
@@ -155,6 +163,13 @@ def launch_target_items(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q
     return default_target_items() * waves_per_simd(pool, v_pool, n_q, k_mask, v_mask)
 
 
+def launch_lead_ratio(pool: DevicePagePool, v_pool: DevicePagePool | None, n_q: int, k_mask: int | None = None,
+                      v_mask: int | None = None) -> float | None:
+    """``LEAD_RATIO`` when the instance for these formats runs two waves per
+    SIMD (plan lead-trail items for it), else None."""
+    return LEAD_RATIO if waves_per_simd(pool, v_pool, n_q, k_mask, v_mask) == 2 else None
+
+
 def choose_pages_per_split(seq_pages: np.ndarray, n_kv_heads: int, target_items: int | None = None) -> int:
     """Smallest pages-per-split (at least MIN_PAGES_PER_SPLIT) for which the
     plan has at most ``target_items`` items; the planner then cuts every
@@ -217,7 +232,7 @@ def page_costs(k_pool: DevicePagePool, v_pool: DevicePagePool, k_table, v_table,
 
 def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *, device="cuda",
               target_items: int | None = None, chunks_per_page: int = 1, page_cost=None,
-              last_page_tokens=None) -> DecodePlan:
+              last_page_tokens=None, lead_ratio: float | None = None) -> DecodePlan:
     """Work and merge items for a batch with these page counts.  With
     ``pages_per_split`` the near-equal splits of ``dc_plan_decode`` (whole
     pages).  Without it ``dc_plan_decode_fill``: ``target_items`` (default:
@@ -230,7 +245,10 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     ``last_page_tokens`` (one per sequence, fill plans only): the tokens in
     each sequence's last page, so the chunks past them are not counted and
     no item falls among them; without it every page counts as full.
-    ``DecodePlan.pages_per_split`` is the largest item's page count."""
+    ``DecodePlan.pages_per_split`` is the largest item's page count.
+    ``lead_ratio`` (fill plans for an instance at two waves per SIMD): a
+    lead-trail plan (:func:`lead_trail_split`) of ``target_items / 2`` SIMD
+    shares."""
     torch = _torch()
     sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
     if sp.ndim != 1 or sp.size == 0:
@@ -253,11 +271,14 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
         last = np.ascontiguousarray(np.asarray(last_page_tokens, dtype=np.int32))
         if last.shape != sp.shape:
             raise ValueError("last_page_tokens must have one entry per sequence")
+    lead = float(lead_ratio) if (fill and lead_ratio) else None
     key = (sp.tobytes(), int(n_kv_heads), pps, target, cpp, None if cost is None else (cost.shape, cost.tobytes()),
-           None if last is None else last.tobytes(), str(device))
+           None if last is None else last.tobytes(), lead, str(device))
     hit = _plan_cache.get(key)
     if hit is not None:
         return hit
+    if lead:
+        target = max(target // 2, 1)  # SIMD shares, each cut into a lead and a trail item
     L = _lib.lib()
     ni, nm, npart, big = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
 
@@ -283,14 +304,79 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
         pps = -(-int(big.value) // cpp)
     host_items = np.frombuffer(bytes(items), dtype=np.int32).reshape(-1, 8)[: ni.value].copy()
     host_merges = np.frombuffer(bytes(merges), dtype=np.int32).reshape(-1, 4)[: nm.value].copy()
-    dev_items = torch.frombuffer(bytearray(bytes(items)), dtype=torch.uint8).to(device)
-    dev_merges = torch.frombuffer(bytearray(bytes(merges)), dtype=torch.uint8).to(device) if nm.value else None
-    plan = DecodePlan(dev_items, dev_merges, ni.value, nm.value, npart.value, pps, host_items, host_merges,
+    n_part = npart.value
+    if lead:
+        host_items = lead_trail_split(host_items, lead, cpp)
+        host_items, host_merges, n_part = _stream_partials(host_items, int(n_kv_heads))
+        big.value = int(_item_chunks(host_items, cpp).max())
+        pps = -(-int(big.value) // cpp)
+    dev_items = torch.from_numpy(host_items.ravel().view(np.uint8).copy()).to(device)
+    dev_merges = torch.from_numpy(host_merges.ravel().view(np.uint8).copy()).to(device) if len(host_merges) else None
+    plan = DecodePlan(dev_items, dev_merges, len(host_items), len(host_merges), n_part, pps, host_items, host_merges,
                       chunks_per_page=cpp, largest_chunks=int(big.value) if fill else pps)
     if len(_plan_cache) > 256:
         _plan_cache.clear()
     _plan_cache[key] = plan
     return plan
+
+
+def _item_chunks(items: np.ndarray, cpp: int) -> np.ndarray:
+    """32-token chunks of each host work item (``[n, 8]``)."""
+    it = np.asarray(items, dtype=np.int64).reshape(-1, 8)
+    first = it[:, 2] * cpp + it[:, 5]
+    end = np.where(it[:, 6] > 0, (it[:, 3] - 1) * cpp + it[:, 6], it[:, 3] * cpp)
+    return end - first
+
+
+def lead_trail_split(items: np.ndarray, ratio: float, cpp: int) -> np.ndarray:
+    """Cut each host work item (one SIMD's share) at a chunk boundary into
+    a lead item ``ratio`` times the trail item's chunks and the trail item;
+    the leads first, in order, then the unsplit shares, then the trails in
+    the leads' order, so trail j follows the launch's n leads at block n + j
+    and shares lead j's SIMD.  A share of one chunk stays whole.  (The only
+    share of a short stream is cut too, although its stream then needs a
+    merge: left whole it ran alone on its SIMD and set the end of the
+    launch, C4 39.3 -> 47.0 us.)  Partial slots are not set."""
+    it = np.asarray(items, dtype=np.int64).reshape(-1, 8)
+    first = it[:, 2] * cpp + it[:, 5]
+    n = _item_chunks(it, cpp)
+    cut = first + np.clip(np.rint(n * float(ratio) / (1.0 + float(ratio))).astype(np.int64), 1, np.maximum(n - 1, 1))
+    split = n >= 2
+
+    def rng(seq, head, u0, u1):
+        return [seq, head, u0 // cpp, -(-u1 // cpp), -1, u0 % cpp, u1 % cpp, 0]
+
+    leads, whole, trails = [], [], []
+    for k in range(len(it)):
+        seq, head = int(it[k, 0]), int(it[k, 1])
+        u0, u1 = int(first[k]), int(first[k] + n[k])
+        if split[k]:
+            leads.append(rng(seq, head, u0, int(cut[k])))
+            trails.append(rng(seq, head, int(cut[k]), u1))
+        else:
+            whole.append(rng(seq, head, u0, u1))
+    return np.asarray(leads + whole + trails, dtype=np.int32).reshape(-1, 8)
+
+
+def _stream_partials(items: np.ndarray, n_kv_heads: int, force_merge: bool = False):
+    """Partial slots and merge items for host work items in any order:
+    every (sequence, KV head) stream's items take consecutive slots and one
+    merge item; a stream of one item writes its output directly (unless
+    ``force_merge``).  Returns (items, merges [m, 4], n_partials)."""
+    items = np.asarray(items, dtype=np.int32).reshape(-1, 8).copy()
+    H = int(n_kv_heads)
+    stream = items[:, 0].astype(np.int64) * H + items[:, 1]
+    merges, n_part = [], 0
+    for s_ in np.unique(stream):
+        rows = np.flatnonzero(stream == s_)
+        if len(rows) == 1 and not force_merge:
+            items[rows[0], 4] = -1
+            continue
+        items[rows, 4] = n_part + np.arange(len(rows), dtype=np.int32)
+        merges.append((int(s_) // H, int(s_) % H, n_part, len(rows)))
+        n_part += len(rows)
+    items[:, 7] = 0
+    return items, np.asarray(merges, dtype=np.int32).reshape(-1, 4), n_part
 
 
 def _fill_units(unit_pages: np.ndarray, unit_last: np.ndarray, unit_cost, cpp: int, target: int,
@@ -322,7 +408,8 @@ def _fill_units(unit_pages: np.ndarray, unit_last: np.ndarray, unit_cost, cpp: i
 
 def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks_per_page: int = 1, page_cost=None,
                      last_page_tokens=None, target_items: int | None = None, front_items: int | None = None,
-                     front_min_chunks: int = 1, window_merge: bool = False) -> DecodePlan:
+                     front_min_chunks: int = 1, window_merge: bool = False,
+                     lead_ratio: float | None = None) -> DecodePlan:
     """A fill plan in two launches: pages ``[front[b, 0], front[b, 1])`` of
     every stream of sequence b (``front``: int ``[n_seqs, 2]``, an empty
     range for none) are cut into ``front_items`` items (default: one per
@@ -339,7 +426,8 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
     ``window_merge``: no front launch; the merge of every stream attends its
     front pages itself (``dc_window_merge``: fp16 key and value pages, at
     most 256 tokens in 8 pages per stream), so the plan has one merge item
-    per stream and one launch."""
+    per stream and one launch.  ``lead_ratio``: the bulk launch as a
+    lead-trail plan (:func:`make_plan`)."""
     torch = _torch()
     sp = np.ascontiguousarray(np.asarray(seq_pages, dtype=np.int32))
     if sp.ndim != 1 or sp.size == 0 or np.any(sp <= 0):
@@ -365,7 +453,7 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
         if np.any((fr[:, 0] == 0) & (fr[:, 1] == sp)):
             raise ValueError("window_merge: every stream needs pages outside its window")
     key = ("region", sp.tobytes(), H, fr.tobytes(), cpp, None if cost is None else cost.tobytes(), last.tobytes(),
-           target, front_items, int(front_min_chunks), bool(window_merge), str(device))
+           target, front_items, int(front_min_chunks), bool(window_merge), lead_ratio, str(device))
     hit = _plan_cache.get(key)
     if hit is not None:
         return hit
@@ -399,23 +487,16 @@ def make_region_plan(seq_pages, n_kv_heads: int, front, *, device="cuda", chunks
         front_items = sum((p1 - p0 - 1) * cpp + (min(cpp, (int(last[b]) + 31) // 32) if p1 == sp[b] else cpp)
                           for b, h, p0, p1 in front_units)
     f_it, f_big = plan_units(front_units, int(front_items), int(front_min_chunks))
-    b_it, b_big = plan_units(bulk_units, target, MIN_CHUNKS_PER_SPLIT)
+    b_it, b_big = plan_units(bulk_units, max(target // 2, 1) if lead_ratio else target, MIN_CHUNKS_PER_SPLIT)
+    if lead_ratio and len(b_it):
+        b_it = lead_trail_split(b_it, float(lead_ratio), cpp)
+        b_big = int(_item_chunks(b_it, cpp).max())
     items = np.concatenate([f_it, b_it]) if len(f_it) else b_it
     # partial slots: every stream's items (front and bulk) take consecutive
     # slots, merged by one merge item; a stream of one item writes its output
     # (with window_merge every stream has a merge item: it attends the window)
-    stream = items[:, 0].astype(np.int64) * H + items[:, 1]
-    merges, n_part = [], 0
-    for s in np.unique(stream):
-        rows = np.flatnonzero(stream == s)
-        if len(rows) == 1 and not window_merge:
-            items[rows[0], 4] = -1
-            continue
-        items[rows, 4] = n_part + np.arange(len(rows), dtype=np.int32)
-        merges.append((int(s) // H, int(s) % H, n_part, len(rows)))
-        n_part += len(rows)
-    items[:, 7] = 0
-    host_merges = np.asarray(merges, dtype=np.int32).reshape(-1, 4)
+    items, host_merges, n_part = _stream_partials(items, H, force_merge=window_merge)
+    merges = host_merges
     dev_items = torch.from_numpy(items.ravel().view(np.uint8).copy()).to(device)
     dev_merges = torch.from_numpy(host_merges.ravel().view(np.uint8).copy()).to(device) if len(merges) else None
     big = max(f_big, b_big)
@@ -641,7 +722,8 @@ def decode_paged(
         if validate:  # the host tables are at hand: cut only chunks that hold tokens
             last = np.asarray([pool.tokens_of(kt[b, 0, sp[b] - 1]) for b in range(B)], dtype=np.int32)
         plan = make_plan(sp, H, pages_per_split, device=queries.device, chunks_per_page=cpp,
-                         target_items=launch_target_items(pool, vpool, Q), last_page_tokens=last)
+                         target_items=launch_target_items(pool, vpool, Q), last_page_tokens=last,
+                         lead_ratio=launch_lead_ratio(pool, vpool, Q))
     plan.check(sp, H, stride, cpp)
     if not queries.is_contiguous():
         queries = queries.contiguous()

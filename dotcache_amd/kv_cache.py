@@ -36,7 +36,8 @@ import numpy as np
 
 from . import _lib
 from .config import DotCacheConfig, observe_page
-from .decode import chunks_per_page, decode_paged, launch_target_items, make_plan, make_region_plan, workspace_bytes
+from .decode import (chunks_per_page, decode_paged, launch_lead_ratio, launch_target_items, make_plan, make_region_plan,
+                     workspace_bytes)
 from .encode import make_header, resolve_encode_spec
 from .page_pool import DevicePagePool, PoolGeometry, page_format_of
 
@@ -309,11 +310,13 @@ class DevicePagedKVCache:
             masks = (self.k_pool.format_mask_of(kt[outside]), self.v_pool.format_mask_of(vt[outside]))
             plan = make_region_plan(seq_pages, H, front, device=self.device, chunks_per_page=cpp,
                                     target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H, *masks),
-                                    last_page_tokens=last_tokens, window_merge=True)
+                                    last_page_tokens=last_tokens, window_merge=True,
+                                    lead_ratio=launch_lead_ratio(self.k_pool, self.v_pool, Hq // H, *masks))
         else:
             plan = make_plan(seq_pages, H, device=self.device, chunks_per_page=cpp,
                              target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H),
-                             last_page_tokens=last_tokens)
+                             last_page_tokens=last_tokens,
+                             lead_ratio=launch_lead_ratio(self.k_pool, self.v_pool, Hq // H))
         need = workspace_bytes(plan, Hq // H, hd)
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.device)

@@ -15,8 +15,8 @@ import numpy as np
 
 from . import _lib
 from .config import PageModeSpec, choose_page_mode, make_explicit_policy
-from .decode import (DecodePlan, chunks_per_page, decode_paged, gather_records, launch_target_items, make_plan,
-                     make_region_plan, merge_partials, page_costs, workspace_bytes)
+from .decode import (DecodePlan, chunks_per_page, decode_paged, gather_records, launch_lead_ratio, launch_target_items,
+                     make_plan, make_region_plan, merge_partials, page_costs, workspace_bytes)
 from .page_pool import DevicePagePool, PoolGeometry
 
 
@@ -128,6 +128,7 @@ class Workload:
     new_v: list = field(default_factory=list)
     plan: DecodePlan | None = None  # layer 0's plan (every layer's when a split is given)
     plans: list = field(default_factory=list)  # per layer: items of near-equal cost under its page formats
+    lead_ratios: list = field(default_factory=list)  # per layer: the plan's lead/trail ratio (None: plain)
     records: list = field(default_factory=list)  # per layer: page records of its plan (PageRecords)
     outs: list = field(default_factory=list)
     workspace: object = None
@@ -279,7 +280,7 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
                    context: int | None = None, pages_per_split: int | None = None,
                    scatter_pages: bool = True, key_bits: int | None = None,
                    replicas: int | None = None, window: str = "merge",
-                   front_items: int | None = None) -> Workload:
+                   front_items: int | None = None, lead_ratio: float | None | str = "auto") -> Workload:
     """Encode every layer's pages on the device and build its page tables.
     ``layers`` / ``batch`` / ``context`` shrink the workload for tests (one
     KV set unless ``replicas`` says otherwise); ``replicas`` sets the number
@@ -292,7 +293,9 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
     ``"launch"`` in a decode launch of its own ahead of the rest
     (``front_items`` items, default one per chunk), either way keeping the
     decode launch to the kernel instance of its 4-bit pages; ``"none"``
-    decodes them with the rest in one launch."""
+    decodes them with the rest in one launch; ``lead_ratio`` (fill plans):
+    "auto" plans lead-trail items where the instance runs two waves per
+    SIMD (``launch_lead_ratio``), a number that ratio there, None never."""
     if window not in ("merge", "launch", "none"):
         raise ValueError("window must be 'merge', 'launch' or 'none'")
     torch = _torch()
@@ -430,6 +433,15 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
     # bytes per token)
     # (the last pages' token counts: C5's tail holds the one appended token)
     cpp = chunks_per_page(P)
+
+    def _lead(kp, vp, q, km=None, vm=None):
+        if pages_per_split is not None or lead_ratio is None or launch_lead_ratio(kp, vp, q, km, vm) is None:
+            r = None
+        else:
+            r = launch_lead_ratio(kp, vp, q, km, vm) if lead_ratio == "auto" else float(lead_ratio)
+        wl.lead_ratios.append(r)
+        return r
+
     for l, lt in enumerate(tables):
         cost = None
         if pages_per_split is None:
@@ -449,11 +461,16 @@ def build_workload(name: str, *, seed: int = 0, device="cuda", layers: int | Non
             wl.plans.append(make_region_plan(lt.seq_pages, H, front, device=dev, chunks_per_page=cpp, page_cost=cost,
                                              target_items=launch_target_items(k_pool, v_pool, Q, km, vm),
                                              last_page_tokens=last, front_items=front_items,
-                                             window_merge=window == "merge"))
+                                             window_merge=window == "merge",
+                                             lead_ratio=_lead(k_pool, v_pool, Q, km, vm)))
         else:
+            # (page records will narrow the launch to the formats its tables
+            # reference: plan for that instance)
+            km = k_pool.format_mask_of(kids_by_layer[l])
+            vm = v_pool.format_mask_of(vids_by_layer[l])
             wl.plans.append(make_plan(lt.seq_pages, H, pages_per_split, device=dev, chunks_per_page=cpp,
-                                      page_cost=cost, target_items=launch_target_items(k_pool, v_pool, Q),
-                                      last_page_tokens=last))
+                                      page_cost=cost, target_items=launch_target_items(k_pool, v_pool, Q, km, vm),
+                                      last_page_tokens=last, lead_ratio=_lead(k_pool, v_pool, Q, km, vm)))
     wl.plan = wl.plans[0]
     need = max(workspace_bytes(p, Q, hd) for p in wl.plans)
     wl.workspace = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)

@@ -62,3 +62,37 @@ def test_region_plan_rejects_bad_ranges():
         make_region_plan(sp, 1, np.array([[0, 5], [0, 1]]), device="cpu", chunks_per_page=2)
     with pytest.raises(ValueError):
         make_region_plan(sp, 1, np.array([[3, 2], [0, 1]]), device="cpu", chunks_per_page=2)
+
+
+@pytest.mark.parametrize("ratio", [1.0, 1.6, 3.0])
+def test_lead_trail_plans_cover_each_chunk_once(ratio):
+    """Lead-trail plans (instances at two waves per SIMD): the first half of
+    the items are the SIMD shares' leads, the second half their trails in
+    the same order, each pair cut from one share at about ratio : 1, and
+    the chunks covered are exactly a plain plan's."""
+    from dotcache_amd.decode import _item_chunks, make_plan
+
+    sp = np.array([40, 7, 300, 33, 1], dtype=np.int32)
+    H, cpp = 2, 2
+    last = np.array([64, 10, 33, 64, 5], dtype=np.int32)
+    plain = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=32, last_page_tokens=last)
+    lt = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=64, last_page_tokens=last,
+                   lead_ratio=ratio)
+    assert sorted(_chunks(plain.host_items, cpp)) == sorted(_chunks(lt.host_items, cpp))
+    n_share = plain.n_items
+    lead, trail = lt.host_items[:n_share], lt.host_items[n_share:]
+    # every share of two or more chunks became a (lead, trail) pair; those
+    # leads come first, in order, then the one-chunk shares, then the
+    # trails in the leads' order
+    pi = plain.host_items
+    big = _item_chunks(pi, cpp) >= 2
+    assert len(trail) == int(big.sum()) and int(big.sum()) < n_share
+    c_lead, c_trail = _item_chunks(lead[: len(trail)], cpp), _item_chunks(trail, cpp)
+    assert np.array_equal(lead[: len(trail), :2], trail[:, :2])
+    assert np.array_equal(lead[: len(trail), :2], pi[big, :2])
+    assert np.all(np.abs(c_lead - ratio * c_trail) <= ratio + 1)
+    assert np.array_equal(lead[len(trail):, :2], pi[~big, :2])
+    lt.check(sp, H, 300, cpp)
+    for seq, head, first, count in lt.host_merges:
+        rows = np.flatnonzero((lt.host_items[:, 0] == seq) & (lt.host_items[:, 1] == head))
+        assert sorted(lt.host_items[rows, 4].tolist()) == list(range(first, first + count))
