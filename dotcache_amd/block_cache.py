@@ -29,7 +29,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from .config import DotCacheConfig
-from .decode import chunks_per_page, decode_paged, launch_target_items, make_plan, workspace_bytes
+from .decode import decode_paged, plan_decode, workspace_bytes
 from .encode import resolve_encode_spec
 from .kv_cache import default_q_head_to_kv_head
 from .page_pool import DevicePagePool, PoolGeometry, page_format_of
@@ -278,15 +278,18 @@ class DeviceVllmPagedKVCache:
         qg = (q if contiguous else q[:, order_t]).reshape(B, H, Hq // H, hd)
         seq_pages = n_blocks.astype(np.int32)
         last_tokens = np.asarray([self._fill[lid][bt_host[b, n_blocks[b] - 1]] for b in range(B)], dtype=np.int32)
-        plan = make_plan(seq_pages, H, device=self.device,
-                         chunks_per_page=chunks_per_page(self.k_pool.geometry.page_capacity),
-                         target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H),
-                         last_page_tokens=last_tokens)
+        # (a sequence's live block is an fp16 page: the split-K merge attends
+        # it, and the decode launch takes the instance of the full blocks)
+        kt = self._map["K"][lid][np.clip(bt_host, 0, nmap - 1)].transpose(0, 2, 1)
+        vt = self._map["V"][lid][np.clip(bt_host, 0, nmap - 1)].transpose(0, 2, 1)
+        plan, masks = plan_decode(self.k_pool, self.v_pool, kt, vt, seq_pages, Hq // H, device=self.device,
+                                  last_page_tokens=last_tokens)
         need = workspace_bytes(plan, Hq // H, hd)
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.device)
         out = decode_paged(self.k_pool, k_table, v_table, seq_pages, qg, query_scale=query_scale, plan=plan,
-                           workspace=self._workspace, validate=False, v_pool=self.v_pool).reshape(B, Hq, hd)
+                           workspace=self._workspace, validate=False, v_pool=self.v_pool,
+                           page_masks=masks).reshape(B, Hq, hd)
         if contiguous:
             return out
         res = torch.empty_like(out)

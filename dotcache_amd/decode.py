@@ -619,6 +619,61 @@ def gather_records(pool: DevicePagePool, k_table, v_table, seq_pages, plan: Deco
                        PageRecords.versions_of(k_table, v_table, pool, vpool), k_mask, v_mask, fk, fv, win)
 
 
+def merge_windows(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray,
+                  seq_pages) -> np.ndarray | None:
+    """Per sequence, pages ``[begin, end)`` of host tables ``kt`` / ``vt``
+    that a window merge can attend: the trailing run of fp16 key and value
+    pages (a cache's tail or live block, and young pages the recent window
+    kept exact), the same for every KV head, at most 8 pages and 256 tokens
+    after at least one other page; ``[end, end)`` for a sequence with none.
+    None when some sequence's run does not qualify or none has one, or the
+    head_dim is not one ``dc_window_merge`` takes."""
+    if pool.geometry.head_dim not in (64, 128, 256):
+        return None
+    f16 = _lib.FMT_M3_F16
+    out = np.zeros((kt.shape[0], 2), dtype=np.int64)
+    for b in range(kt.shape[0]):
+        n = int(seq_pages[b])
+        exact = (pool.formats_of(kt[b, :, :n]) == f16) & (vpool.formats_of(vt[b, :, :n]) == f16)
+        if not np.all(exact == exact[0]):
+            return None
+        run = n - int(np.flatnonzero(~exact[0])[-1]) - 1 if not exact[0].all() else n
+        begin = n - run
+        if run and (begin == 0 or run > 8 or int(pool.tokens_of(kt[b, 0, begin:n]).sum()) > 256):
+            return None
+        out[b] = (begin, n)
+    return out if np.any(out[:, 1] > out[:, 0]) else None
+
+
+def plan_decode(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray, seq_pages, n_q: int, *,
+                device="cuda", last_page_tokens=None) -> tuple[DecodePlan, tuple[int, int]]:
+    """The fill plan for a decode over host page tables ``kt`` / ``vt``
+    (``[n_seqs, n_kv_heads, stride]``) and the format masks of its decode
+    launch, for ``decode_paged(plan=..., page_masks=...)``: a region plan
+    with merge windows (:func:`merge_windows`) when the sequences end in
+    fp16 pages, so the launch takes the kernel instance of the other pages'
+    formats; lead-trail items where that instance runs two waves per SIMD."""
+    sp = np.asarray(seq_pages, dtype=np.int64)
+    H = kt.shape[1]
+    cpp = chunks_per_page(pool.geometry.page_capacity)
+    front = merge_windows(pool, vpool, kt, vt, sp)
+    pg = np.arange(kt.shape[2])[None, None, :]
+    read = pg < sp[:, None, None]
+    if front is not None:
+        read = read & ~((pg >= front[:, 0, None, None]) & (pg < front[:, 1, None, None]))
+    read = np.broadcast_to(read, kt.shape)
+    masks = (pool.format_mask_of(kt[read]) & pool.format_mask, vpool.format_mask_of(vt[read]) & vpool.format_mask)
+    target = launch_target_items(pool, vpool, n_q, *masks)
+    lead = launch_lead_ratio(pool, vpool, n_q, *masks)
+    if front is not None:
+        plan = make_region_plan(sp, H, front, device=device, chunks_per_page=cpp, target_items=target,
+                                last_page_tokens=last_page_tokens, window_merge=True, lead_ratio=lead)
+    else:
+        plan = make_plan(sp, H, device=device, chunks_per_page=cpp, target_items=target,
+                         last_page_tokens=last_page_tokens, lead_ratio=lead)
+    return plan, masks
+
+
 def check_windows(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray, plan: DecodePlan) -> None:
     """Raise ValueError unless every window of ``plan`` (``window_merge``)
     holds only fp16 (M3 f16) key and value pages of equal token counts, the

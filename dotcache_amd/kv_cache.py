@@ -34,10 +34,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import _lib
 from .config import DotCacheConfig, observe_page
-from .decode import (chunks_per_page, decode_paged, launch_lead_ratio, launch_target_items, make_plan, make_region_plan,
-                     workspace_bytes)
+from .decode import decode_paged, plan_decode, workspace_bytes
 from .encode import make_header, resolve_encode_spec
 from .page_pool import DevicePagePool, PoolGeometry, page_format_of
 
@@ -297,26 +295,11 @@ class DevicePagedKVCache:
         kt, vt = self._host_tables[lid]
         qg = q if contiguous else q[:, torch.from_numpy(order).to(self.device)]
         queries = qg.reshape(B, H, Hq // H, hd)
-        cpp = chunks_per_page(self.k_pool.geometry.page_capacity)
         # The fp16 tail page (and any young exact pages right before it) is
         # attended by the split-K merge, so the decode launch takes the kernel
         # instance of the other pages' formats (region plan, merge windows).
-        front = self._merge_windows(kt, vt, seq_pages)
-        masks = None
-        if front is not None:
-            pg = np.arange(kt.shape[2])[None, None, :]
-            outside = np.broadcast_to((pg < seq_pages[:, None, None])
-                                      & ~((pg >= front[:, 0, None, None]) & (pg < front[:, 1, None, None])), kt.shape)
-            masks = (self.k_pool.format_mask_of(kt[outside]), self.v_pool.format_mask_of(vt[outside]))
-            plan = make_region_plan(seq_pages, H, front, device=self.device, chunks_per_page=cpp,
-                                    target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H, *masks),
-                                    last_page_tokens=last_tokens, window_merge=True,
-                                    lead_ratio=launch_lead_ratio(self.k_pool, self.v_pool, Hq // H, *masks))
-        else:
-            plan = make_plan(seq_pages, H, device=self.device, chunks_per_page=cpp,
-                             target_items=launch_target_items(self.k_pool, self.v_pool, Hq // H),
-                             last_page_tokens=last_tokens,
-                             lead_ratio=launch_lead_ratio(self.k_pool, self.v_pool, Hq // H))
+        plan, masks = plan_decode(self.k_pool, self.v_pool, kt, vt, seq_pages, Hq // H, device=self.device,
+                                  last_page_tokens=last_tokens)
         need = workspace_bytes(plan, Hq // H, hd)
         if self._workspace is None or self._workspace.numel() < need:
             self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.device)
@@ -328,29 +311,6 @@ class DevicePagedKVCache:
         res = torch.empty_like(out)
         res[:, torch.from_numpy(order).to(self.device)] = out
         return res
-
-    def _merge_windows(self, kt: np.ndarray, vt: np.ndarray, seq_pages: np.ndarray) -> np.ndarray | None:
-        """Per sequence, pages ``[begin, end)``: the trailing run of fp16 key
-        and value pages (the tail, and young exact pages before it), the
-        same for every KV head, at most 8 pages and 256 tokens after at
-        least one other page; ``[end, end)`` for a sequence with none.  None
-        when some sequence's run does not qualify (the decode then reads
-        every page in one launch) or no sequence has one."""
-        if self.config.head_dim not in (64, 128, 256):  # (the head dims dc_window_merge takes)
-            return None
-        f16 = _lib.FMT_M3_F16
-        out = np.zeros((kt.shape[0], 2), dtype=np.int64)
-        for b in range(kt.shape[0]):
-            n = int(seq_pages[b])
-            exact = (self.k_pool.formats_of(kt[b, :, :n]) == f16) & (self.v_pool.formats_of(vt[b, :, :n]) == f16)
-            if not np.all(exact == exact[0]):
-                return None
-            run = n - int(np.flatnonzero(~exact[0])[-1]) - 1 if not exact[0].all() else n
-            begin = n - run
-            if run and (begin == 0 or run > 8 or int(self.k_pool.tokens_of(kt[b, 0, begin:n]).sum()) > 256):
-                return None
-            out[b] = (begin, n)
-        return out if np.any(out[:, 1] > out[:, 0]) else None
 
     # ---- bookkeeping -------------------------------------------------------
     def _layer_tables(self, lid: int):

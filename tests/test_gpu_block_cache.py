@@ -144,5 +144,15 @@ def test_decode_block_tables_batches_ragged_sequences():
             want = O.decode_grouped(q[b, h * G:(h + 1) * G][None], [kp], [vp])[0]
             err = np.max(np.abs(got[b, h * G:(h + 1) * G] - want))
             assert err < 3e-4, f"sequence {b} head {h}: max-abs error {err}"
+    # sequences 0 and 1 alone: sequence 0's live block is attended by the
+    # split-K merge (a window), and the result is the same
+    from dotcache_amd.decode import merge_windows
+
+    kt = cache._map["K"][0][bt[:2].clip(0)].transpose(0, 2, 1)
+    vt = cache._map["V"][0][bt[:2].clip(0)].transpose(0, 2, 1)
+    front = merge_windows(cache.k_pool, cache.v_pool, kt, vt, np.array([3, 1]))
+    assert front is not None and front.tolist() == [[2, 3], [1, 1]]
+    got2 = cache.decode_block_tables(0, torch.from_numpy(q[:2]), torch.from_numpy(bt[:2]), lens[:2]).cpu().numpy()
+    assert np.max(np.abs(got2 - got[:2])) < 2e-5
     with pytest.raises(ValueError):
         cache.decode_block_tables(0, torch.from_numpy(q), torch.from_numpy(bt), [150, 64, 8])  # block 25 holds 7

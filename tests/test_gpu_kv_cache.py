@@ -122,8 +122,10 @@ def test_prefill_append_decode_matches_oracle(page_tokens, case):
     # the fp16 tail (5 tokens) was attended by the split-K merge, and the
     # decode launch read only the other pages (with 16-token pages under the
     # recent window every page is exact: one launch reads them all)
+    from dotcache_amd.decode import merge_windows
+
     k_table, _, seq_pages, _ = cache._layer_tables(0)
-    front = cache._merge_windows(*cache._host_tables[0], seq_pages)
+    front = merge_windows(cache.k_pool, cache.v_pool, *cache._host_tables[0], seq_pages)
     if case == "mode_override" or P == 64:
         assert front is not None and np.all(front[:, 1] == seq_pages) and np.all(front[:, 0] >= 1)
     else:
