@@ -131,6 +131,9 @@ def test_chunk_cut_plans_match_oracle(kfmt, vfmt, vgs, hd, Q, tpp, path):
             cost = rng.uniform(0.2, 3.0, size=(len(counts), 1, int(counts.max()))).astype(np.float32)
             plans.append((f"fill {target}", make_plan(counts, 1, device="cuda", target_items=target,
                                                       chunks_per_page=cpp, page_cost=cost)))
+        for ratio in (1.6, 3.0):  # lead-trail plans (instances at two waves per SIMD)
+            plans.append((f"lead-trail {ratio}", make_plan(counts, 1, device="cuda", target_items=18,
+                                                           chunks_per_page=cpp, lead_ratio=ratio)))
         for cuts in (1, 3, 12):
             plans.append((f"random {cuts}", _random_plan(rng, counts, cpp, cuts)))
         if cpp > 1:
