@@ -1544,6 +1544,9 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   DC_EXACT(256, 32, KEYS_M3, 4, 4, true, false, false, 4)  // config 5's window launch (fp16 keys and values)
   DC_EXACT(128, 32, KEYS_M0, 8, 4, false, true, true, 4)  // 8-bit keys, 4-bit values
   DC_EXACT(128, 32, KEYS_M0, 8, 8, false, true, true, 4)  // 8-bit keys and values
+  DC_EXACT(128, 64, KEYS_M0, 8, 8, false, true, false, 8)     // config 4 with 8-bit keys
+  DC_EXACT(128, 64, KEYS_MIXED, 8, 8, false, true, false, 8)
+  DC_EXACT(256, 32, KEYS_M0, 8, 4, false, true, true, 4)      // config 5 with 8-bit keys (decode launch)
   DC_GENERAL(64, 32, 4)
   DC_GENERAL(64, 32, 8)
   DC_GENERAL(64, 64, 4)
