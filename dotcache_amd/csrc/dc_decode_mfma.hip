@@ -1529,10 +1529,16 @@ int launch_decode_mfma(const DecodeArgs& a, hipStream_t stream, bool* launched) 
   if (rc < 0 && hd == HD_ && vgs == VGS_ && kmode == KM_ && (KM_ == KEYS_M3 || kbits == KB_) &&          \
       vbits == VB_ && vm3 == VM3_ && kaff == KA_ && vaff == VA_)                                         \
     rc = launch_q<HD_, VGS_, KM_, KB_, VB_, VM3_, KA_, VA_, QM_>(a, stream);
-#define DC_GENERAL(HD_, VGS_, VB_)                                                    \
-  if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_)                             \
-    rc = kbits == 8 ? launch_t<HD_, VGS_, KEYS_MIXED, 8, VB_, true, true, true>(a, stream) \
-                    : launch_t<HD_, VGS_, KEYS_MIXED, 4, VB_, true, true, true>(a, stream);
+// (general instances take head blocks from the smallest their group counts
+// allow: 4 heads where key and value groups come in fours, 8 in twos)
+#define DC_GENERAL(HD_, VGS_, VB_)                                                                  \
+  if (rc < 0 && hd == HD_ && vgs == VGS_ && vbits == VB_) {                                         \
+    constexpr int kq = (HD_ / 32) % 4 == 0 && (HD_ / VGS_) % 4 == 0   ? 4                            \
+                       : (HD_ / 32) % 2 == 0 && (HD_ / VGS_) % 2 == 0 ? 8                            \
+                                                                      : 16;                          \
+    rc = kbits == 8 ? launch_q<HD_, VGS_, KEYS_MIXED, 8, VB_, true, true, true, kq>(a, stream)      \
+                    : launch_q<HD_, VGS_, KEYS_MIXED, 4, VB_, true, true, true, kq>(a, stream);     \
+  }
   DC_EXACT(64, 32, KEYS_M0, 4, 4, false, false, false, 8)     // config 1
   DC_EXACT(64, 32, KEYS_M0, 4, 4, false, true, true, 8)       // config 2
   DC_EXACT(128, 32, KEYS_M3, 4, 4, false, false, false, 16)   // config 3 (blocks of 8: slower)
