@@ -447,14 +447,20 @@ def main():
     # (the KV sets are cycled here as in the steps, so every launch reads
     # its pages from HBM)
     R = wl.replicas
+    # each kernel-only graph holds at least 28 launches (the layers of `reps`
+    # consecutive KV sets), so that a short replay is not timed at the host's
+    # graph-launch rate (C1 has one launch per step)
+    reps = max(1, -(-28 // L))
 
     def decode_set(r):
-        for l in wl.replica_layers(r):
-            wl.decode_kernel(l)
+        for k in range(reps):
+            for l in wl.replica_layers((r + k) % R):
+                wl.decode_kernel(l)
 
     def merge_set(r):
-        for l in wl.replica_layers(r):
-            wl.merge_kernel(l)
+        for k in range(reps):
+            for l in wl.replica_layers((r + k) % R):
+                wl.merge_kernel(l)
 
     if args.eager:
         dec_fns = [lambda r=r: decode_set(r) for r in range(R)]
@@ -483,8 +489,8 @@ def main():
             fn()
     torch.cuda.synchronize()
     lead = max(10, args.warmup)
-    dec_ms = per_call(decode_all, n_med, lead) / L
-    merge_ms_all = per_call(merge_all, n_med, lead) / L
+    dec_ms = per_call(decode_all, n_med, lead) / (L * reps)
+    merge_ms_all = per_call(merge_all, n_med, lead) / (L * reps)
     # roofline.achieved uses the mean launch time (what a kernel trace's
     # average gives); the median is reported beside it
     launch_ms = float(np.mean(dec_ms))
@@ -568,7 +574,8 @@ def main():
                          if wl.plan.n_front else " (dc_decode_paged, one launch per layer"
                          + ("; the exact window is read by the merge)" if wl.plan.host_windows is not None else ")")),
             "launch_us": launch_ms * 1e3,
-            "launch_us_stat": f"mean over {n_med} replays of one step's {L} decode launches (event per replay)",
+            "launch_us_stat": f"mean over {n_med} replays of {L * reps} decode launches ({reps} step(s) of {L}; "
+                              "event per replay)",
             "launch_us_median": float(np.median(dec_ms)) * 1e3,
             "launch_us_p10_p90": [float(np.percentile(dec_ms, 10)) * 1e3, float(np.percentile(dec_ms, 90)) * 1e3],
             "frac_at_median_launch": bytes_launch / (float(np.median(dec_ms)) / 1e3) / 1e9 / HBM_PEAK_GBPS,
