@@ -290,6 +290,7 @@ def test_fused_decode_peaked_attention_and_small_values():
 # "divisible" and "permuted" wrong ones that must fall back.
 MERGE_LAYOUTS = {
     "ragged": ([5, 1, 40, 3], None, 2),
+    "long": ([70, 1, 150, 3], None, 1),  # passes of 2 and 4 slots per row, several of 4
     "uniform": ([6, 6, 6, 6], None, 0),
     "divisible": ([5, 1, 10, 8], None, 0),
     "permuted": ([6, 6, 6, 6], [6, 0, 18, 12], 0),
