@@ -639,7 +639,7 @@ def merge_windows(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, v
             return None
         run = n - int(np.flatnonzero(~exact[0])[-1]) - 1 if not exact[0].all() else n
         begin = n - run
-        if run and (begin == 0 or run > 8 or int(pool.tokens_of(kt[b, 0, begin:n]).sum()) > 256):
+        if run and (begin == 0 or run > 8 or int(pool.tokens_of(kt[b, :, begin:n]).sum(axis=-1).max()) > 256):
             return None
         out[b] = (begin, n)
     return out if np.any(out[:, 1] > out[:, 0]) else None
@@ -677,7 +677,8 @@ def plan_decode(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt:
 def check_windows(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray, plan: DecodePlan) -> None:
     """Raise ValueError unless every window of ``plan`` (``window_merge``)
     holds only fp16 (M3 f16) key and value pages of equal token counts, the
-    only pages ``dc_window_merge`` reads (it skips others)."""
+    only pages ``dc_window_merge`` reads (it skips others), and at most 8
+    pages and 256 tokens (it would attend only the first 256)."""
     for (seq, head, _, _), (pb, pe) in zip(np.asarray(plan.host_merges).reshape(-1, 4),
                                            np.asarray(plan.host_windows).reshape(-1, 2)):
         if pe <= pb:
@@ -688,6 +689,8 @@ def check_windows(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, v
         if (np.any(pool.formats_of(kid) != _lib.FMT_M3_F16) or np.any(vpool.formats_of(vid) != _lib.FMT_M3_F16)
                 or not np.array_equal(pool.tokens_of(kid), vpool.tokens_of(vid))):
             raise ValueError("a merge window holds a page that is not an fp16 (M3) key / value page pair")
+        if pe - pb > 8 or int(pool.tokens_of(kid).sum()) > 256:
+            raise ValueError("a merge window holds more than 8 pages or 256 tokens")
 
 
 def items_format_masks(pool: DevicePagePool, vpool: DevicePagePool, kt: np.ndarray, vt: np.ndarray,

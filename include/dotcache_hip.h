@@ -393,7 +393,10 @@ int dc_lse_merge(const dc_merge_item* merges, int32_t n_merges, const void* work
  * launch of their own, and the decode launch keeps the kernel instance of
  * the 4-bit pages.  A window holds at most 256 tokens in at most 8 pages;
  * head_dim must be 64, 128 or 256; out and the workspace 16-byte aligned.
- * Pages of another format in a window are skipped (hosts validate them).
+ * The windows are device data, so the kernel guards them: a range of more
+ * than 8 pages or past table_stride is skipped whole, tokens past a
+ * window's 256th and pages of another format are skipped (hosts validate
+ * windows first: dotcache_amd.decode.check_windows).
  * records: NULL, or device [n_merges][8] key / value descriptor pairs of
  * each window's pages in order (a host snapshot of the tables and
  * descriptors), read instead of the tables and descriptor arrays.

@@ -107,3 +107,43 @@ def test_window_merge_rejects_non_fp16_windows():
                             last_page_tokens=np.array([10], np.int32))
     with pytest.raises(ValueError, match="fp16"):
         decode_paged(kprep[0].pool, kt, vt, [4], q, plan=plan, v_pool=vprep[0].pool, validate=True)
+
+
+def test_window_bound_holds_on_every_head():
+    """merge_windows bounds a window's tokens on every KV head: here head
+    0's fp16 run holds 120 tokens and head 1's 276, past the 256 a window
+    merge attends, so plan_decode takes a plan without windows, and the
+    decode still matches the oracle."""
+    import torch
+
+    from dotcache_amd.backends import prepare_pages_hip
+    from dotcache_amd.decode import decode_paged, merge_windows, plan_decode
+
+    rng = np.random.default_rng(7)
+    hd, Q = 128, 3
+    kw = dict(head_dim=hd, group_size=32)
+
+    def head_pages(kind, win):  # one full 4-bit page, then fp16 pages of these token counts
+        m0 = dict(bits=4, scheme="affine" if kind == "K" else "symmetric")
+        pages = O.encode_pages(hard_values(rng, 256, hd), tokens_per_page=256, kind=kind, **kw, **m0)
+        for t in win:
+            pages += O.encode_pages(rng.normal(size=(t, hd)).astype(np.float32), tokens_per_page=t, mode="M3",
+                                    kind=kind, **kw)
+        return pages
+
+    kp = [head_pages("K", (100, 20)), head_pages("K", (256, 20))]
+    vp = [head_pages("V", (100, 20)), head_pages("V", (256, 20))]
+    kprep = prepare_pages_hip([to_product_page(p) for g in kp for p in g])
+    vprep = prepare_pages_hip([to_product_page(p) for g in vp for p in g])
+    pool, vpool = kprep[0].pool, vprep[0].pool
+    kt = np.asarray([p.page_id for p in kprep], np.int32).reshape(1, 2, 3)
+    vt = np.asarray([p.page_id for p in vprep], np.int32).reshape(1, 2, 3)
+    assert merge_windows(pool, vpool, kt, vt, [3]) is None
+    plan, masks = plan_decode(pool, vpool, kt, vt, [3], Q, device="cuda", last_page_tokens=np.array([20], np.int32))
+    assert plan.host_windows is None
+    q32 = (rng.normal(size=(1, 2, Q, hd)) / np.sqrt(hd)).astype(np.float32)
+    want = O.decode_grouped(q32.reshape(-1, Q, hd), kp, vp).reshape(1, 2, Q, hd)
+    out = decode_paged(pool, torch.from_numpy(kt).cuda(), torch.from_numpy(vt).cuda(), [3], torch.from_numpy(q32).cuda(),
+                       plan=plan, v_pool=vpool, page_masks=masks)
+    err = float(np.max(np.abs(out.cpu().numpy() - want)))
+    assert err < TOL, f"decode vs oracle {err}"
