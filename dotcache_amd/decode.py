@@ -49,6 +49,11 @@ CHUNK_COST_BYTES = 8192
 # into a lead item, placed in the first half of the launch, and a trail
 # item this many times smaller in the second.
 LEAD_RATIO = 1.6
+# A wave alone on its SIMD streams about this fraction of what the SIMD's
+# two waves stream together: in those equal-item C4 launches the second wave
+# ran alone for the last 7 of 33 us.  Lead-trail plans use it to price a
+# SIMD whose two items do not end together (``_pair_time``).
+LONE_WAVE_RATE = 0.86
 
 
 def _torch():
@@ -306,7 +311,10 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
     host_merges = np.frombuffer(bytes(merges), dtype=np.int32).reshape(-1, 4)[: nm.value].copy()
     n_part = npart.value
     if lead:
-        host_items = lead_trail_split(host_items, lead, cpp)
+        pairs = []
+        if fill:
+            host_items, pairs = _pair_short_streams(host_items, sp, int(n_kv_heads), cpp, last, cost, target, lead)
+        host_items = lead_trail_split(host_items, lead, cpp, pairs=pairs)
         host_items, host_merges, n_part = _stream_partials(host_items, int(n_kv_heads))
         big.value = int(_item_chunks(host_items, cpp).max())
         pps = -(-int(big.value) // cpp)
@@ -328,15 +336,17 @@ def _item_chunks(items: np.ndarray, cpp: int) -> np.ndarray:
     return end - first
 
 
-def lead_trail_split(items: np.ndarray, ratio: float, cpp: int) -> np.ndarray:
+def lead_trail_split(items: np.ndarray, ratio: float, cpp: int, pairs=()) -> np.ndarray:
     """Cut each host work item (one SIMD's share) at a chunk boundary into
     a lead item ``ratio`` times the trail item's chunks and the trail item;
     the leads first, in order, then the unsplit shares, then the trails in
-    the leads' order, so trail j follows the launch's n leads at block n + j
-    and shares lead j's SIMD.  A share of one chunk stays whole.  (The only
-    share of a short stream is cut too, although its stream then needs a
-    merge: left whole it ran alone on its SIMD and set the end of the
-    launch, C4 39.3 -> 47.0 us.)  Partial slots are not set."""
+    the leads' order, so trail j follows the launch's n shares at block n +
+    j and shares lead j's SIMD.  A share of one chunk stays whole.  (The
+    only share of a short stream is cut too, although its stream then needs
+    a merge: left whole it ran alone on its SIMD and set the end of the
+    launch, C4 39.3 -> 47.0 us.)  ``pairs``: (lead, trail) host items of
+    shares made of two whole streams (``_pair_short_streams``), placed after
+    the cut shares' leads and trails.  Partial slots are not set."""
     it = np.asarray(items, dtype=np.int64).reshape(-1, 8)
     first = it[:, 2] * cpp + it[:, 5]
     n = _item_chunks(it, cpp)
@@ -355,7 +365,110 @@ def lead_trail_split(items: np.ndarray, ratio: float, cpp: int) -> np.ndarray:
             trails.append(rng(seq, head, int(cut[k]), u1))
         else:
             whole.append(rng(seq, head, u0, u1))
+    leads += [list(map(int, a)) for a, _ in pairs]
+    trails += [list(map(int, b)) for _, b in pairs]
     return np.asarray(leads + whole + trails, dtype=np.int32).reshape(-1, 8)
+
+
+def _pair_time(a: float, b: float, ratio: float) -> float:
+    """Time of a SIMD running items of costs a (the older wave, which issues
+    first) and b at two waves per SIMD, in units of one cost unit at the
+    SIMD's two-wave rate: a share cut at ``ratio`` : 1 takes a + b; an item
+    left alone after the other ends runs at ``LONE_WAVE_RATE``."""
+    lf = ratio / (1.0 + ratio)  # the lead's part of the SIMD's rate while both run
+    if a >= ratio * b:
+        return b / (1.0 - lf) + (a - ratio * b) / LONE_WAVE_RATE
+    return a / lf + (b - a * (1.0 - lf) / lf) / LONE_WAVE_RATE
+
+
+def _stream_chunk_costs(sp: np.ndarray, n_kv_heads: int, cpp: int, last, cost) -> list[np.ndarray]:
+    """Cost of every chunk that holds tokens, per stream s = b * H + h: a
+    page's cost spread over its chunks (1 per chunk without page costs),
+    as ``dc_plan_decode_fill`` prices them."""
+    out = []
+    for b in range(sp.size):
+        lc = cpp if last is None else min(cpp, (int(last[b]) + 31) // 32)
+        per_page = np.full(int(sp[b]), cpp, dtype=np.int64)
+        per_page[-1] = lc
+        for h in range(n_kv_heads):
+            if cost is None:
+                out.append(np.ones(int(per_page.sum())))
+            else:
+                c = np.asarray(cost[b, h, : sp[b]], dtype=np.float64)
+                out.append(np.repeat(c / per_page, per_page))
+    return out
+
+
+def _items_cost(items: np.ndarray, chunk_costs: list[np.ndarray], n_kv_heads: int, cpp: int) -> np.ndarray:
+    it = np.asarray(items, dtype=np.int64).reshape(-1, 8)
+    first = it[:, 2] * cpp + it[:, 5]
+    end = first + _item_chunks(it, cpp)
+    return np.asarray([chunk_costs[int(b) * n_kv_heads + int(h)][int(u0):int(u1)].sum()
+                       for (b, h), u0, u1 in zip(it[:, :2], first, end)])
+
+
+def _pair_short_streams(items: np.ndarray, sp: np.ndarray, n_kv_heads: int, cpp: int, last, cost, n_shares: int,
+                        ratio: float):
+    """A fill plan of ``n_shares`` SIMD shares (``items``, one stream per
+    share) gives every stream a whole number of shares, so its largest share
+    exceeds the mean by up to a chunk (C4: 28 chunks against a mean of
+    25.7), while a short stream's only share holds less.  Two short whole
+    streams may share one SIMD instead, the longer as the lead (the older
+    wave) and the shorter as the trail, freeing a share for the long
+    streams, and the paired streams, each one item, need no merge.  Returns
+    (items of the other streams' fill plan, [(lead, trail) host items])
+    for the pairing whose largest SIMD time (``_pair_time``) is lowest and
+    no higher than the plain plan's, the most pairs among equals; else
+    (``items``, []).  (C4: 12 pairs, the decode launch 39.4-39.7 against
+    39.3-39.6 us, the merge 4.6 against 5.1 us with 24 fewer merge items.)"""
+    H = n_kv_heads
+    ccost = _stream_chunk_costs(sp, H, cpp, last, cost)
+    total = np.asarray([c.sum() for c in ccost])
+    if len(items) < n_shares or total.size < 3:
+        return items, []
+    level = float(_items_cost(items, ccost, H, cpp).max())
+    unit = float(total.sum()) / sum(c.size for c in ccost)  # mean chunk cost
+    mean = float(total.sum()) / n_shares
+    short = [int(s) for s in np.argsort(-total, kind="stable") if total[s] < level]
+
+    def whole(s):
+        b, h = divmod(s, H)
+        n = ccost[s].size
+        return [b, h, 0, -(-n // cpp), -1, 0, n % cpp, 0]
+
+    best = (level, 0, items, [])
+    bound = level
+    while bound >= mean:
+        used, pairs = set(), []
+        for i, s in enumerate(short):
+            if s in used:
+                continue
+            for t in short[i + 1:]:  # the longest partner whose pair time fits
+                if t not in used and _pair_time(total[s], total[t], ratio) <= bound:
+                    used |= {s, t}
+                    pairs.append((s, t))
+                    break
+        if not pairs:
+            break
+        rest = [s for s in range(total.size) if s not in used]
+        units = [(s // H, s % H, 0, int(sp[s // H])) for s in rest]
+        u = np.asarray(units, dtype=np.int64)
+        pages = (u[:, 3] - u[:, 2]).astype(np.int32)
+        ulast = (np.full(len(u), 32 * cpp, np.int32) if last is None else np.asarray(last)[u[:, 0]]).astype(np.int32)
+        ucost = None
+        if cost is not None:
+            ucost = np.zeros((len(u), 1, int(pages.max())), dtype=np.float32)
+            for k, (b, h, p0, p1) in enumerate(u):
+                ucost[k, 0, : p1 - p0] = cost[b, h, p0:p1]
+        it, _ = _fill_units(pages, ulast, ucost, cpp, n_shares - len(pairs), MIN_CHUNKS_PER_SPLIT)
+        src = u[it[:, 0]]
+        it[:, 0], it[:, 1] = src[:, 0], src[:, 1]
+        worst = max(float(_items_cost(it, ccost, H, cpp).max()),
+                    max(_pair_time(total[s], total[t], ratio) for s, t in pairs))
+        if (worst, -len(pairs)) < (best[0], -best[1]):
+            best = (worst, len(pairs), it, [(whole(s), whole(t)) for s, t in pairs])
+        bound -= unit
+    return best[2], best[3]
 
 
 def _stream_partials(items: np.ndarray, n_kv_heads: int, force_merge: bool = False):

@@ -65,26 +65,21 @@ def test_region_plan_rejects_bad_ranges():
 
 
 @pytest.mark.parametrize("ratio", [1.0, 1.6, 3.0])
-def test_lead_trail_plans_cover_each_chunk_once(ratio):
-    """Lead-trail plans (instances at two waves per SIMD): the first half of
-    the items are the SIMD shares' leads, the second half their trails in
-    the same order, each pair cut from one share at about ratio : 1, and
-    the chunks covered are exactly a plain plan's."""
-    from dotcache_amd.decode import _item_chunks, make_plan
+def test_lead_trail_split_layout(ratio):
+    """lead_trail_split on a plain plan's shares: the first items are the
+    shares' leads, then the one-chunk shares, then the trails in the same
+    order, each pair cut from one share at about ratio : 1, covering
+    exactly the shares' chunks."""
+    from dotcache_amd.decode import _item_chunks, lead_trail_split, make_plan
 
     sp = np.array([40, 7, 300, 33, 1], dtype=np.int32)
     H, cpp = 2, 2
     last = np.array([64, 10, 33, 64, 5], dtype=np.int32)
-    plain = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=32, last_page_tokens=last)
-    lt = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=64, last_page_tokens=last,
-                   lead_ratio=ratio)
-    assert sorted(_chunks(plain.host_items, cpp)) == sorted(_chunks(lt.host_items, cpp))
-    n_share = plain.n_items
-    lead, trail = lt.host_items[:n_share], lt.host_items[n_share:]
-    # every share of two or more chunks became a (lead, trail) pair; those
-    # leads come first, in order, then the one-chunk shares, then the
-    # trails in the leads' order
-    pi = plain.host_items
+    pi = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=32, last_page_tokens=last).host_items
+    lt = lead_trail_split(pi, ratio, cpp)
+    assert sorted(_chunks(pi, cpp)) == sorted(_chunks(lt, cpp))
+    n_share = len(pi)
+    lead, trail = lt[:n_share], lt[n_share:]
     big = _item_chunks(pi, cpp) >= 2
     assert len(trail) == int(big.sum()) and int(big.sum()) < n_share
     c_lead, c_trail = _item_chunks(lead[: len(trail)], cpp), _item_chunks(trail, cpp)
@@ -92,7 +87,77 @@ def test_lead_trail_plans_cover_each_chunk_once(ratio):
     assert np.array_equal(lead[: len(trail), :2], pi[big, :2])
     assert np.all(np.abs(c_lead - ratio * c_trail) <= ratio + 1)
     assert np.array_equal(lead[len(trail):, :2], pi[~big, :2])
-    lt.check(sp, H, 300, cpp)
+
+
+def _check_lead_trail_plan(lt, plain, sp, H, cpp, stride):
+    """A lead-trail plan covers the plain plan's chunks once; its first
+    n_share items (one per SIMD share) are followed by trails, trail j
+    sharing item j's SIMD: either the rest of item j's share (same stream,
+    the chunks right after the lead's) or, in a pair, a whole stream no
+    longer than the whole-stream lead.  Returns the number of pairs."""
+    from dotcache_amd.decode import _item_chunks
+
+    it = lt.host_items
+    assert sorted(_chunks(plain.host_items, cpp)) == sorted(_chunks(it, cpp))
+    n_share = plain.n_items
+    n_trail = len(it) - n_share
+    assert 0 < n_trail <= n_share
+    ch = _item_chunks(it, cpp)
+    first = it[:, 2].astype(np.int64) * cpp + it[:, 5]
+    stream = it[:, 0].astype(np.int64) * H + it[:, 1]
+    n_items = np.bincount(stream, minlength=len(sp) * H)
+    pairs = 0
+    for j in range(n_trail):
+        a, b = it[j], it[n_share + j]
+        if stream[j] == stream[n_share + j]:
+            assert first[n_share + j] == first[j] + ch[j]  # the trail starts where the lead ends
+        else:
+            pairs += 1
+            assert n_items[stream[j]] == 1 and n_items[stream[n_share + j]] == 1
+            assert a[4] == -1 and b[4] == -1 and ch[j] >= ch[n_share + j]
+    lt.check(sp, H, stride, cpp)
     for seq, head, first, count in lt.host_merges:
-        rows = np.flatnonzero((lt.host_items[:, 0] == seq) & (lt.host_items[:, 1] == head))
-        assert sorted(lt.host_items[rows, 4].tolist()) == list(range(first, first + count))
+        rows = np.flatnonzero((it[:, 0] == seq) & (it[:, 1] == head))
+        assert sorted(it[rows, 4].tolist()) == list(range(first, first + count))
+    return pairs
+
+
+@pytest.mark.parametrize("ratio", [1.0, 1.6, 3.0])
+def test_lead_trail_plans_cover_each_chunk_once(ratio):
+    """make_plan(lead_ratio=...) on a small ragged batch."""
+    from dotcache_amd.decode import make_plan
+
+    sp = np.array([40, 7, 300, 33, 1], dtype=np.int32)
+    H, cpp = 2, 2
+    last = np.array([64, 10, 33, 64, 5], dtype=np.int32)
+    plain = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=32, last_page_tokens=last)
+    lt = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=64, last_page_tokens=last,
+                   lead_ratio=ratio)
+    _check_lead_trail_plan(lt, plain, sp, H, cpp, 300)
+
+
+def test_lead_trail_plans_pair_short_streams():
+    """The C4 batch (64 sequences, 256 to 32768 tokens, two KV heads): short
+    streams share SIMDs in pairs, which lowers the largest modelled SIMD
+    time below the plain lead-trail plan's and leaves those streams without
+    a merge."""
+    from dotcache_amd.decode import _item_chunks, _pair_time, lead_trail_split, make_plan, LONE_WAVE_RATE
+    from dotcache_amd.workloads import SPECS, context_lengths
+
+    ctx = context_lengths(SPECS["c4"], 0)
+    sp = ((ctx + 63) // 64).astype(np.int32)
+    last = (ctx - (sp - 1) * 64).astype(np.int32)
+    H, cpp, n_simd = 2, 2, 1024
+    plain = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=n_simd, last_page_tokens=last)
+    lt = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=2 * n_simd, last_page_tokens=last,
+                   lead_ratio=1.6)
+    assert _check_lead_trail_plan(lt, plain, sp, H, cpp, int(sp.max())) > 0
+
+    def worst(items):
+        ch = _item_chunks(items, cpp).astype(float)
+        nt = len(items) - n_simd
+        return max(_pair_time(ch[j], ch[n_simd + j], 1.6) if j < nt else ch[j] / LONE_WAVE_RATE
+                   for j in range(n_simd))
+
+    assert worst(lt.host_items) < worst(lead_trail_split(plain.host_items, 1.6, cpp))
+    assert lt.n_merges < len(sp) * H
