@@ -381,30 +381,36 @@ def _pair_time(a: float, b: float, ratio: float) -> float:
     return a / lf + (b - a * (1.0 - lf) / lf) / LONE_WAVE_RATE
 
 
-def _stream_chunk_costs(sp: np.ndarray, n_kv_heads: int, cpp: int, last, cost) -> list[np.ndarray]:
-    """Cost of every chunk that holds tokens, per stream s = b * H + h: a
-    page's cost spread over its chunks (1 per chunk without page costs),
-    as ``dc_plan_decode_fill`` prices them."""
-    out = []
+def _stream_cost_prefix(sp: np.ndarray, n_kv_heads: int, cpp: int, last, cost):
+    """Running costs over each stream's chunks that hold tokens, streams s =
+    b * H + h laid end to end: (flat, off, n) with flat[off[s] + u] the cost
+    of stream s's chunks [0, u) and n[s] its chunk count.  A page's cost is
+    spread over its chunks (1 per chunk without page costs), as
+    ``dc_plan_decode_fill`` prices them."""
+    parts, off, n = [], [], []
+    at = 0
     for b in range(sp.size):
         lc = cpp if last is None else min(cpp, (int(last[b]) + 31) // 32)
         per_page = np.full(int(sp[b]), cpp, dtype=np.int64)
         per_page[-1] = lc
         for h in range(n_kv_heads):
             if cost is None:
-                out.append(np.ones(int(per_page.sum())))
+                c = np.ones(int(per_page.sum()))
             else:
-                c = np.asarray(cost[b, h, : sp[b]], dtype=np.float64)
-                out.append(np.repeat(c / per_page, per_page))
-    return out
+                c = np.repeat(np.asarray(cost[b, h, : sp[b]], dtype=np.float64) / per_page, per_page)
+            parts.append(np.concatenate([[0.0], np.cumsum(c)]))
+            off.append(at)
+            n.append(c.size)
+            at += c.size + 1
+    return np.concatenate(parts), np.asarray(off, dtype=np.int64), np.asarray(n, dtype=np.int64)
 
 
-def _items_cost(items: np.ndarray, chunk_costs: list[np.ndarray], n_kv_heads: int, cpp: int) -> np.ndarray:
+def _items_cost(items: np.ndarray, prefix, n_kv_heads: int, cpp: int) -> np.ndarray:
+    flat, off, _ = prefix
     it = np.asarray(items, dtype=np.int64).reshape(-1, 8)
     first = it[:, 2] * cpp + it[:, 5]
-    end = first + _item_chunks(it, cpp)
-    return np.asarray([chunk_costs[int(b) * n_kv_heads + int(h)][int(u0):int(u1)].sum()
-                       for (b, h), u0, u1 in zip(it[:, :2], first, end)])
+    base = off[it[:, 0] * n_kv_heads + it[:, 1]]
+    return flat[base + first + _item_chunks(it, cpp)] - flat[base + first]
 
 
 def _pair_short_streams(items: np.ndarray, sp: np.ndarray, n_kv_heads: int, cpp: int, last, cost, n_shares: int,
@@ -415,59 +421,84 @@ def _pair_short_streams(items: np.ndarray, sp: np.ndarray, n_kv_heads: int, cpp:
     25.7), while a short stream's only share holds less.  Two short whole
     streams may share one SIMD instead, the longer as the lead (the older
     wave) and the shorter as the trail, freeing a share for the long
-    streams, and the paired streams, each one item, need no merge.  Returns
-    (items of the other streams' fill plan, [(lead, trail) host items])
-    for the pairing whose largest SIMD time (``_pair_time``) is lowest and
-    no higher than the plain plan's, the most pairs among equals; else
-    (``items``, []).  (C4: 12 pairs, the decode launch 39.4-39.7 against
-    39.3-39.6 us, the merge 4.6 against 5.1 us with 24 fewer merge items.)"""
+    streams, and the paired streams, each one item, need no merge.  Pairs
+    are formed under a bound on their SIMD time (``_pair_time``), found by
+    bisection between the mean share and the plain plan's largest, where
+    the long streams' largest share meets it.  Returns (items of the other
+    streams' fill plan, [(lead, trail) host items]) for the pairing whose
+    largest SIMD time is lowest and no higher than the plain plan's, the
+    most pairs among equals; else (``items``, []).  (C4: 12 pairs, the
+    decode launch 39.4-39.7 against 39.3-39.6 us, the merge 4.6 against 5.1
+    us with 24 fewer merge items.)"""
     H = n_kv_heads
-    ccost = _stream_chunk_costs(sp, H, cpp, last, cost)
-    total = np.asarray([c.sum() for c in ccost])
-    if len(items) < n_shares or total.size < 3:
+    if len(items) < n_shares or not 3 <= sp.size * H < n_shares:  # (more streams than shares: no spare SIMD)
         return items, []
-    level = float(_items_cost(items, ccost, H, cpp).max())
-    unit = float(total.sum()) / sum(c.size for c in ccost)  # mean chunk cost
+    prefix = _stream_cost_prefix(sp, H, cpp, last, cost)
+    flat, off, nch = prefix
+    total = flat[off + nch]
+    level = float(_items_cost(items, prefix, H, cpp).max())
     mean = float(total.sum()) / n_shares
     short = [int(s) for s in np.argsort(-total, kind="stable") if total[s] < level]
+    if len(short) < 2:
+        return items, []
 
     def whole(s):
         b, h = divmod(s, H)
-        n = ccost[s].size
+        n = int(nch[s])
         return [b, h, 0, -(-n // cpp), -1, 0, n % cpp, 0]
 
-    best = (level, 0, items, [])
-    bound = level
-    while bound >= mean:
+    def evaluate(bound):
+        # longest first, each with the longest partner whose pair time fits:
+        # the partners left are kept by ascending cost, all at most the
+        # current stream's, over which the pair time only grows
+        avail = short[::-1]
         used, pairs = set(), []
-        for i, s in enumerate(short):
-            if s in used:
-                continue
-            for t in short[i + 1:]:  # the longest partner whose pair time fits
-                if t not in used and _pair_time(total[s], total[t], ratio) <= bound:
-                    used |= {s, t}
-                    pairs.append((s, t))
-                    break
+        while avail:
+            s = avail.pop()
+            lo, hi = 0, len(avail)
+            while lo < hi:  # first partner whose pair time exceeds the bound
+                mid = (lo + hi) // 2
+                if _pair_time(total[s], total[avail[mid]], ratio) <= bound:
+                    lo = mid + 1
+                else:
+                    hi = mid
+            if lo > 0:
+                t = avail.pop(lo - 1)
+                used |= {s, t}
+                pairs.append((s, t))
         if not pairs:
-            break
-        rest = [s for s in range(total.size) if s not in used]
-        units = [(s // H, s % H, 0, int(sp[s // H])) for s in rest]
-        u = np.asarray(units, dtype=np.int64)
-        pages = (u[:, 3] - u[:, 2]).astype(np.int32)
-        ulast = (np.full(len(u), 32 * cpp, np.int32) if last is None else np.asarray(last)[u[:, 0]]).astype(np.int32)
+            return None
+        rest = np.asarray([s for s in range(total.size) if s not in used], dtype=np.int64)
+        b_, h_ = rest // H, rest % H
+        pages = sp[b_].astype(np.int32)
+        ulast = (np.full(len(rest), 32 * cpp, np.int32) if last is None else np.asarray(last)[b_]).astype(np.int32)
         ucost = None
         if cost is not None:
-            ucost = np.zeros((len(u), 1, int(pages.max())), dtype=np.float32)
-            for k, (b, h, p0, p1) in enumerate(u):
-                ucost[k, 0, : p1 - p0] = cost[b, h, p0:p1]
+            ucost = np.zeros((len(rest), 1, int(pages.max())), dtype=np.float32)
+            for k in range(len(rest)):
+                ucost[k, 0, : pages[k]] = cost[b_[k], h_[k], : pages[k]]
         it, _ = _fill_units(pages, ulast, ucost, cpp, n_shares - len(pairs), MIN_CHUNKS_PER_SPLIT)
-        src = u[it[:, 0]]
-        it[:, 0], it[:, 1] = src[:, 0], src[:, 1]
-        worst = max(float(_items_cost(it, ccost, H, cpp).max()),
-                    max(_pair_time(total[s], total[t], ratio) for s, t in pairs))
-        if (worst, -len(pairs)) < (best[0], -best[1]):
-            best = (worst, len(pairs), it, [(whole(s), whole(t)) for s, t in pairs])
-        bound -= unit
+        src = rest[it[:, 0]]
+        it[:, 0], it[:, 1] = src // H, src % H
+        return (float(_items_cost(it, prefix, H, cpp).max()),
+                max(_pair_time(total[s], total[t], ratio) for s, t in pairs), pairs, it)
+
+    best = (level, 0, items, [])
+    lo, hi, bound = mean, level, level  # the most pairs first, then four bisection steps
+    for _ in range(5):
+        r = evaluate(bound)
+        if r is None:
+            lo = bound
+        else:
+            longest, pair_max, pairs, it = r
+            worst = max(longest, pair_max)
+            if (worst, -len(pairs)) < (best[0], -best[1]):
+                best = (worst, len(pairs), it, [(whole(s), whole(t)) for s, t in pairs])
+            if longest > bound:  # the long streams are still above it: allow more pairs
+                lo = bound
+            else:
+                hi = bound
+        bound = 0.5 * (lo + hi)
     return best[2], best[3]
 
 
