@@ -283,11 +283,11 @@ def test_fused_decode_peaked_attention_and_small_values():
     assert np.max(np.abs(got - want)) < 1e-3
 
 
-# Merge layouts: (counts, begins or None for in order, unused slots).  The
-# merge kernel takes partials [b c, (b + 1) c) for merge b without waiting
-# for the merge item when the partial slots are a multiple c of the merge
-# count, and checks that guess against the item: "uniform" is a right guess,
-# "divisible" and "permuted" wrong ones that must fall back.
+# Merge layouts: (counts, begins or None for in order, unused slots): ragged
+# counts with spare slots, counts that need several passes of a block's
+# rows, equal counts, counts whose total divides evenly among the merges
+# without being equal, and merges whose partial ranges are not in merge
+# order.
 MERGE_LAYOUTS = {
     "ragged": ([5, 1, 40, 3], None, 2),
     "long": ([70, 1, 150, 3], None, 1),  # passes of 2 and 4 slots per row, several of 4
