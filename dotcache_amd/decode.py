@@ -466,9 +466,9 @@ def _pair_short_streams(items: np.ndarray, sp: np.ndarray, n_kv_heads: int, cpp:
                 t = avail.pop(lo - 1)
                 used |= {s, t}
                 pairs.append((s, t))
-        if not pairs:
-            return None
         rest = np.asarray([s for s in range(total.size) if s not in used], dtype=np.int64)
+        if not pairs or rest.size == 0:
+            return None
         b_, h_ = rest // H, rest % H
         pages = sp[b_].astype(np.int32)
         ulast = (np.full(len(rest), 32 * cpp, np.int32) if last is None else np.asarray(last)[b_]).astype(np.int32)

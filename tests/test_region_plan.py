@@ -161,3 +161,22 @@ def test_lead_trail_plans_pair_short_streams():
 
     assert worst(lt.host_items) < worst(lead_trail_split(plain.host_items, 1.6, cpp))
     assert lt.n_merges < len(sp) * H
+
+
+@pytest.mark.parametrize("sp,H,target", [([6] * 6, 1, 32), ([6, 6, 1, 1, 1, 1], 1, 32), ([2] * 40, 1, 64),
+                                         ([50, 1, 1, 1, 1, 2, 2], 2, 64), ([300, 3, 3, 9, 1], 4, 64)])
+def test_lead_trail_plans_on_edge_batches(sp, H, target):
+    """Lead-trail plans (with or without paired streams) on batches of only
+    short streams, of one long stream among one-page ones, and with more
+    shares than chunks to fill them: every chunk once, trails aligned."""
+    from dotcache_amd.decode import make_plan
+
+    sp = np.asarray(sp, dtype=np.int32)
+    cpp = 2
+    plain = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=target // 2)
+    lt = make_plan(sp, H, device="cpu", chunks_per_page=cpp, target_items=target, lead_ratio=1.6)
+    if len(lt.host_items) > plain.n_items:
+        _check_lead_trail_plan(lt, plain, sp, H, cpp, int(sp.max()))
+    else:
+        assert sorted(_chunks(plain.host_items, cpp)) == sorted(_chunks(lt.host_items, cpp))
+        lt.check(sp, H, int(sp.max()), cpp)
