@@ -467,8 +467,10 @@ def _pair_short_streams(items: np.ndarray, sp: np.ndarray, n_kv_heads: int, cpp:
                 used |= {s, t}
                 pairs.append((s, t))
         rest = np.asarray([s for s in range(total.size) if s not in used], dtype=np.int64)
-        if not pairs or rest.size == 0:
-            return None
+        if not pairs:
+            return None  # the bound is below every pair
+        if rest.size == 0:
+            return False  # every stream paired: leave some to the fill planner
         b_, h_ = rest // H, rest % H
         pages = sp[b_].astype(np.int32)
         ulast = (np.full(len(rest), 32 * cpp, np.int32) if last is None else np.asarray(last)[b_]).astype(np.int32)
@@ -489,6 +491,8 @@ def _pair_short_streams(items: np.ndarray, sp: np.ndarray, n_kv_heads: int, cpp:
         r = evaluate(bound)
         if r is None:
             lo = bound
+        elif r is False:
+            hi = bound
         else:
             longest, pair_max, pairs, it = r
             worst = max(longest, pair_max)
