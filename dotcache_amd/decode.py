@@ -276,9 +276,13 @@ def make_plan(seq_pages, n_kv_heads: int, pages_per_split: int | None = None, *,
         last = np.ascontiguousarray(np.asarray(last_page_tokens, dtype=np.int32))
         if last.shape != sp.shape:
             raise ValueError("last_page_tokens must have one entry per sequence")
+        if np.any(last <= 0) or np.any(last > 32 * cpp):
+            raise ValueError(f"last_page_tokens must lie in [1, {32 * cpp}]")
     lead = float(lead_ratio) if (fill and lead_ratio) else None
+    # the plan depends on the last pages only through their chunk counts, so
+    # a decode that appends a token reuses it until a new chunk starts
     key = (sp.tobytes(), int(n_kv_heads), pps, target, cpp, None if cost is None else (cost.shape, cost.tobytes()),
-           None if last is None else last.tobytes(), lead, str(device))
+           None if last is None else ((last + 31) // 32).tobytes(), lead, str(device))
     hit = _plan_cache.get(key)
     if hit is not None:
         return hit

@@ -180,3 +180,20 @@ def test_lead_trail_plans_on_edge_batches(sp, H, target):
     else:
         assert sorted(_chunks(plain.host_items, cpp)) == sorted(_chunks(lt.host_items, cpp))
         lt.check(sp, H, int(sp.max()), cpp)
+
+
+def test_plans_reused_within_a_chunk():
+    """A plan depends on the last pages only through their chunk counts: a
+    decode step that appends a token reuses the cached plan until a new
+    32-token chunk starts; last-page token counts out of range raise."""
+    from dotcache_amd.decode import make_plan
+
+    sp = np.array([9, 4, 30], dtype=np.int32)
+    kw = dict(device="cpu", chunks_per_page=2, target_items=24)
+    a = make_plan(sp, 2, last_page_tokens=np.array([33, 64, 1], np.int32), **kw)
+    b = make_plan(sp, 2, last_page_tokens=np.array([40, 63, 20], np.int32), **kw)
+    c = make_plan(sp, 2, last_page_tokens=np.array([32, 64, 1], np.int32), **kw)
+    assert a is b and a is not c
+    for bad in ([0, 64, 1], [33, 65, 1]):
+        with pytest.raises(ValueError):
+            make_plan(sp, 2, last_page_tokens=np.array(bad, np.int32), **kw)
